@@ -1,0 +1,111 @@
+/* C-ABI of the MI355X-native SOL routed-attention library (libsol_attn_amd.so).
+ *
+ * The reference binds its device work through a Python launch layer
+ * (src/sol_attn_amd/kernels.py:185-225: `_pooled`, `launch_dense`,
+ * `launch_sol`).  These entry points replace that layer one for one; the
+ * public Python API above them (attention.py, indexed.py) is unchanged.
+ *
+ * Conventions
+ *  - Tensors are BF16 (passed as `const void*`), FP32 (`float*`), int32,
+ *    uint8 (bool) or int64, all in device memory of the current HIP device.
+ *  - Q/K/V are addressed as rows of `head_dim` contiguous elements.  Each
+ *    operand takes three element strides {batch, token, head}.  When an index
+ *    pointer ([batch, tokens] int64, device memory) is given, token t of
+ *    batch b is row index[b * tokens + t] and the batch stride is ignored
+ *    (indexed windows, indexed.py:99).
+ *  - Row starts must be 16-byte aligned: base pointers 16-byte aligned and
+ *    strides multiples of 8 elements.
+ *  - The library never allocates or frees device memory.  Launches are
+ *    asynchronous on `stream` (a hipStream_t; NULL = legacy default stream).
+ *  - Return value: 0 on success, negative for an invalid argument (message in
+ *    sol_last_error()), positive = the hipError_t of a failed launch.
+ *  - Calls are stateless and re-entrant; results are deterministic (no
+ *    floating-point atomics; fixed reduction orders).
+ */
+#ifndef SOL_ATTN_AMD_H
+#define SOL_ATTN_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SOL_ABI_VERSION 1
+#define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
+#define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
+
+#define SOL_OK 0
+#define SOL_ERR_INVALID (-1)
+#define SOL_ERR_UNSUPPORTED (-2)
+
+/* ABI version of the loaded library (SOL_ABI_VERSION). */
+int sol_abi_version(void);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* sol_last_error(void);
+
+/* Byte sizes of the pooling outputs for a problem (reference: the torch.empty
+ * calls of kernels.py:187,207,211-212):
+ *   sizes[0] kc          bf16 [batch, heads, NKB, head_dim]
+ *   sizes[1] vct         bf16 [batch, heads, head_dim, NKBP]  (NKBP = NKB rounded up to 32)
+ *   sizes[2] chunk_sums  fp32 [batch, heads, ceil(NKB/16), 2, head_dim]
+ *   sizes[3] key_mean    fp32 [batch, heads, head_dim]  (key_var has the same size)
+ * with NKB = ceil(key_tokens / 64). */
+int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
+                   int64_t sizes[4]);
+
+/* K/V block pooling and diagonal key moments.
+ * Replaces `_pooled(k)`, `_pooled(v)` (kernels.py:185-190, kernel `_pool`
+ * kernels.py:16-27) and `_moments` (kernels.py:30-49).
+ * kc/vct receive BF16 (round-to-nearest-even) 64-token block means; when
+ * key_mean/key_var/chunk_sums are all non-NULL, also the per-(batch, head,
+ * feature) population mean and clamped variance of the BF16 centroids. */
+int sol_pool_kv(const void* k, const int64_t* k_strides,
+                const void* v, const int64_t* v_strides,
+                const int64_t* key_index,
+                int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
+                void* kc, void* vct, float* chunk_sums, float* key_mean, float* key_var,
+                void* stream);
+
+/* Fused routing + attention over pooled keys.
+ * Replaces the `_threshold` and `_sol` launches of `launch_sol`
+ * (kernels.py:203-225; kernels kernels.py:52-64 and 101-182).
+ * beta: finite, -INFINITY (every block exact) or +INFINITY (protected blocks
+ * only); key_mean/key_var are read only for finite beta.  local_blocks < 0
+ * disables the local band (indexed windows).  Sink token counts round
+ * outward to whole blocks.  protection: NULL or uint8 [batch, NQB, NKB].
+ * out: contiguous BF16 [batch, query_tokens, heads, head_dim].
+ * counts: NULL or int32 [batch, NQB, heads] exact-block counts.
+ * debug_selected (uint8) / debug_proxy (fp32): NULL or [batch, NQB, heads, NKB]
+ * routing decisions and proxies (natural-log units); debug_cutoff: NULL or
+ * fp32 [batch, NQB, heads].  Debug outputs are for verification, not timing. */
+int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
+                      const void* k, const int64_t* k_strides,
+                      const void* v, const int64_t* v_strides, const int64_t* key_index,
+                      int64_t batch, int64_t query_tokens, int64_t key_tokens,
+                      int64_t heads, int64_t head_dim,
+                      const void* kc, const void* vct,
+                      const float* key_mean, const float* key_var,
+                      const uint8_t* protection,
+                      double scale, double beta, int64_t local_blocks,
+                      int64_t kv_sink_tokens, int64_t query_sink_tokens,
+                      void* out, int32_t* counts,
+                      uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
+                      void* stream);
+
+/* Non-causal BF16 attention over all keys, FP32 softmax and accumulation.
+ * Replaces `launch_dense` (kernels.py:193-200; kernel kernels.py:67-98).
+ * out: contiguous BF16 [batch, query_tokens, heads, head_dim]. */
+int sol_dense_fwd(const void* q, const int64_t* q_strides,
+                  const void* k, const int64_t* k_strides,
+                  const void* v, const int64_t* v_strides,
+                  int64_t batch, int64_t query_tokens, int64_t key_tokens,
+                  int64_t heads, int64_t head_dim, double scale,
+                  void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOL_ATTN_AMD_H */

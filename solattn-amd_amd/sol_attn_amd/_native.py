@@ -1,0 +1,182 @@
+"""Launch layer over the HIP C-ABI library (replaces the reference's kernels.py).
+
+Mirrors ``src/sol_attn_amd/kernels.py:185-225``: ``launch_sol`` and
+``launch_dense`` take validated BF16 tensors, allocate every output and
+workspace with ``torch.empty`` on the input device, and enqueue the HIP
+kernels on the current stream.  There is no CPU path: when the library is not
+built this module raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+import torch
+
+BLOCK = 64
+MAX_KEY_BLOCKS = 8192
+ABI_VERSION = 1
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
+_lib = None
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_dbl = ctypes.c_double
+
+_SIGNATURES = {
+    "sol_abi_version": ([], ctypes.c_int),
+    "sol_last_error": ([], ctypes.c_char_p),
+    "sol_pool_sizes": ([_i64, _i64, _i64, _i64, _i64p], ctypes.c_int),
+    "sol_pool_kv": ([_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64,
+                     _p, _p, _p, _p, _p, _p], ctypes.c_int),
+    "sol_attention_fwd": ([_p, _i64p, _p, _p, _i64p, _p, _i64p, _p,
+                           _i64, _i64, _i64, _i64, _i64,
+                           _p, _p, _p, _p, _p,
+                           _dbl, _dbl, _i64, _i64, _i64,
+                           _p, _p, _p, _p, _p, _p], ctypes.c_int),
+    "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
+                       _dbl, _p, _p], ctypes.c_int),
+}
+
+
+def library():
+    """Load ``libsol_attn_amd.so`` once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"SOL HIP library not built ({LIB_PATH} missing); "
+                "run `python -m sol_attn_amd._build` or __graft_entry__.build()")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res
+        if lib.sol_abi_version() != ABI_VERSION:
+            raise RuntimeError("libsol_attn_amd.so ABI version mismatch; rebuild it")
+        _lib = lib
+    return _lib
+
+
+def _check(status):
+    if status != 0:
+        msg = library().sol_last_error().decode(errors="replace")
+        raise RuntimeError(f"SOL HIP call failed ({status}): {msg}")
+
+
+def _strides(x, indexed=False):
+    s = x.stride()
+    return (ctypes.c_int64 * 3)(0 if indexed else s[0], s[-3], s[-2])
+
+
+def _ptr(x):
+    return None if x is None else ctypes.c_void_p(x.data_ptr())
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _aligned(x):
+    """Rows start on 16-byte boundaries (base pointer and all strides)."""
+    return x.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in x.stride()[:-1])
+
+
+def _rows(x):
+    # Misaligned views are copied once on the GPU; inputs are never written.
+    return x if _aligned(x) else x.clone(memory_format=torch.contiguous_format)
+
+
+def pool_kv(k, v, key_index=None, moments=True):
+    """K/V centroids (and key moments) as the attention kernel consumes them.
+
+    ``k``/``v``: ``[B, Tk, H, D]`` BF16 or, with ``key_index`` ``[B, Tk]``,
+    NHD ``[N, H, D]``.  Returns a dict with ``kc`` ``[B, H, NKB, D]``,
+    ``vct`` ``[B, H, D, NKBP]``, ``mean``/``var`` ``[B, H, D]`` (or None).
+    """
+    lib = library()
+    indexed = key_index is not None
+    if indexed:
+        b, tk = key_index.shape
+        h, d = k.shape[-2:]
+    else:
+        b, tk, h, d = k.shape
+    k, v = _rows(k), _rows(v)
+    nkb = -(-tk // BLOCK)
+    nkbp = -(-nkb // 32) * 32
+    dev = k.device
+    kc = torch.empty((b, h, nkb, d), device=dev, dtype=torch.bfloat16)
+    vct = torch.empty((b, h, d, nkbp), device=dev, dtype=torch.bfloat16)
+    mean = var = sums = None
+    if moments:
+        sums = torch.empty((b, h, -(-nkb // 16), 2, d), device=dev, dtype=torch.float32)
+        mean = torch.empty((b, h, d), device=dev, dtype=torch.float32)
+        var = torch.empty_like(mean)
+    _check(lib.sol_pool_kv(_ptr(k), _strides(k, indexed), _ptr(v), _strides(v, indexed),
+                           _ptr(key_index), b, tk, h, d, _ptr(kc), _ptr(vct), _ptr(sums),
+                           _ptr(mean), _ptr(var), _stream(dev)))
+    return {"kc": kc, "vct": vct, "mean": mean, "var": var}
+
+
+def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=None,
+               rows=None, keys=None, debug=False):
+    """All-in SOL attention (``kernels.py:203-225``): pooling, moments, routing, attention.
+
+    ``rows``/``keys`` (indexed windows) gather Q and K/V token rows inside the
+    kernels instead of materialising copies.  Returns ``(out, counts)`` and,
+    with ``debug=True``, a dict of routing diagnostics as a third element.
+    """
+    lib = library()
+    finite = not math.isinf(beta)
+    indexed = keys is not None
+    if indexed:
+        b, nq = rows.shape
+        nk = keys.shape[1]
+        h, d = q.shape[-2:]
+    else:
+        b, nq, h, d = q.shape
+        nk = k.shape[1]
+    q, k, v = _rows(q), _rows(k), _rows(v)
+    dev = q.device
+    nqb, nkb = -(-nq // BLOCK), -(-nk // BLOCK)
+    pooled = pool_kv(k, v, key_index=keys, moments=finite)
+    out = torch.empty((b, nq, h, d), device=dev, dtype=torch.bfloat16)
+    counts = torch.empty((b, nqb, h), device=dev, dtype=torch.int32)
+    dbg = None
+    if debug:
+        dbg = {"selected": torch.empty((b, nqb, h, nkb), device=dev, dtype=torch.uint8),
+               "proxy": torch.full((b, nqb, h, nkb), math.nan, device=dev, dtype=torch.float32),
+               "cutoff": torch.empty((b, nqb, h), device=dev, dtype=torch.float32)}
+    prot = None
+    if protection is not None:
+        prot = protection.contiguous().view(torch.uint8)
+    _check(lib.sol_attention_fwd(
+        _ptr(q), _strides(q, indexed), _ptr(rows), _ptr(k), _strides(k, indexed), _ptr(v),
+        _strides(v, indexed), _ptr(keys), b, nq, nk, h, d,
+        _ptr(pooled["kc"]), _ptr(pooled["vct"]), _ptr(pooled["mean"]), _ptr(pooled["var"]),
+        _ptr(prot), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
+        _ptr(out), _ptr(counts),
+        _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
+        _stream(dev)))
+    if debug:
+        dbg["selected"] = dbg["selected"].bool()
+        dbg.update(pooled)
+        return out, counts, dbg
+    return out, counts
+
+
+def launch_dense(q, k, v, scale):
+    """Dense control (``kernels.py:193-200``): non-causal attention over all keys."""
+    lib = library()
+    q, k, v = _rows(q), _rows(k), _rows(v)
+    b, nq, h, d = q.shape
+    out = torch.empty((b, nq, h, d), device=q.device, dtype=torch.bfloat16)
+    _check(lib.sol_dense_fwd(_ptr(q), _strides(q), _ptr(k), _strides(k), _ptr(v), _strides(v),
+                             b, nq, k.shape[1], h, d, float(scale), _ptr(out),
+                             _stream(q.device)))
+    return out

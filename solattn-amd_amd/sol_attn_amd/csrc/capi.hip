@@ -1,0 +1,207 @@
+// extern "C" entry points: argument checks, parameter packing, launches.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "sol_attn_amd.h"
+#include "sol_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_status(hipError_t err) {
+  if (err == hipSuccess) return SOL_OK;
+  g_last_error = std::string("HIP launch failed: ") + hipGetErrorString(err);
+  return int(err);
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks one BF16 operand's base pointer and {batch, token, head} strides.
+bool operand_ok(const void* base, const int64_t* strides, bool indexed) {
+  if (!base || !strides || !aligned16(base)) return false;
+  for (int i = 0; i < 3; ++i) {
+    if (i == 0 && indexed) continue;
+    if (strides[i] <= 0 || strides[i] % 8 != 0) return false;
+  }
+  return true;
+}
+
+bool shape_ok(int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim) {
+  return batch > 0 && tokens > 0 && heads > 0 && (head_dim == 64 || head_dim == 128) &&
+         batch * heads < (int64_t(1) << 24) && tokens < (int64_t(1) << 30);
+}
+
+sol::TokenRows rows_of(const void* base, const int64_t* strides, const int64_t* index, int64_t tokens) {
+  sol::TokenRows r;
+  r.base = static_cast<const uint16_t*>(base);
+  r.index = index;
+  r.sb = strides[0];
+  r.st = strides[1];
+  r.sh = strides[2];
+  r.T = int(tokens);
+  return r;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sol_abi_version(void) { return SOL_ABI_VERSION; }
+
+const char* sol_last_error(void) { return g_last_error.c_str(); }
+
+int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
+                   int64_t sizes[4]) {
+  if (!sizes || !shape_ok(batch, key_tokens, heads, head_dim))
+    return fail(SOL_ERR_INVALID, "sol_pool_sizes: invalid shape");
+  const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
+  const int64_t nkbp = cdiv(nkb, 32) * 32;
+  sizes[0] = batch * heads * nkb * head_dim * 2;
+  sizes[1] = batch * heads * head_dim * nkbp * 2;
+  sizes[2] = batch * heads * cdiv(nkb, 16) * 2 * head_dim * 4;
+  sizes[3] = batch * heads * head_dim * 4;
+  return SOL_OK;
+}
+
+int sol_pool_kv(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                const int64_t* key_index, int64_t batch, int64_t key_tokens, int64_t heads,
+                int64_t head_dim, void* kc, void* vct, float* chunk_sums, float* key_mean,
+                float* key_var, void* stream) {
+  if (!shape_ok(batch, key_tokens, heads, head_dim))
+    return fail(SOL_ERR_INVALID, "sol_pool_kv: unsupported shape (head_dim must be 64 or 128)");
+  const bool indexed = key_index != nullptr;
+  if (!operand_ok(k, k_strides, indexed) || !operand_ok(v, v_strides, indexed))
+    return fail(SOL_ERR_INVALID, "sol_pool_kv: K/V need 16-byte aligned rows and positive strides");
+  if (!kc || !vct || !aligned16(kc) || !aligned16(vct))
+    return fail(SOL_ERR_INVALID, "sol_pool_kv: kc/vct must be 16-byte aligned device buffers");
+  const bool moments = chunk_sums || key_mean || key_var;
+  if (moments && !(chunk_sums && key_mean && key_var))
+    return fail(SOL_ERR_INVALID, "sol_pool_kv: chunk_sums, key_mean and key_var go together");
+  const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
+  if (nkb > (int64_t(1) << 19))
+    return fail(SOL_ERR_UNSUPPORTED, "sol_pool_kv: too many key blocks");
+  sol::PoolParams p;
+  p.k = rows_of(k, k_strides, key_index, key_tokens);
+  p.v = rows_of(v, v_strides, key_index, key_tokens);
+  p.kc = static_cast<uint16_t*>(kc);
+  p.vct = static_cast<uint16_t*>(vct);
+  p.ksum = moments ? chunk_sums : nullptr;
+  p.mean = key_mean;
+  p.var = key_var;
+  p.B = int(batch);
+  p.H = int(heads);
+  p.Tk = int(key_tokens);
+  p.NKB = int(nkb);
+  p.NKBP = int(cdiv(nkb, 32) * 32);
+  p.NCHP = p.NKBP / sol::kPoolChunk;
+  return hip_status(sol::launch_pool(p, int(head_dim), static_cast<hipStream_t>(stream)));
+}
+
+int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
+                      const void* k, const int64_t* k_strides, const void* v,
+                      const int64_t* v_strides, const int64_t* key_index, int64_t batch,
+                      int64_t query_tokens, int64_t key_tokens, int64_t heads, int64_t head_dim,
+                      const void* kc, const void* vct, const float* key_mean,
+                      const float* key_var, const uint8_t* protection, double scale,
+                      double beta, int64_t local_blocks, int64_t kv_sink_tokens,
+                      int64_t query_sink_tokens, void* out, int32_t* counts,
+                      uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
+                      void* stream) {
+  if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
+      key_tokens >= (int64_t(1) << 30))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: unsupported shape (head_dim must be 64 or 128)");
+  if (!operand_ok(q, q_strides, query_index != nullptr) ||
+      !operand_ok(k, k_strides, key_index != nullptr) ||
+      !operand_ok(v, v_strides, key_index != nullptr))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: Q/K/V need 16-byte aligned rows and positive strides");
+  if (!std::isfinite(scale) || scale <= 0)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: scale must be finite and positive");
+  if (std::isnan(beta)) return fail(SOL_ERR_INVALID, "sol_attention_fwd: beta must not be NaN");
+  if (kv_sink_tokens < 0 || query_sink_tokens < 0)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: sink token counts must be nonnegative");
+  const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
+  if (!kc || !vct || !aligned16(kc) || !aligned16(vct) || !out || !aligned16(out))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: kc/vct/out must be 16-byte aligned device buffers");
+  if (force == 0 && (!key_mean || !key_var))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
+  const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
+  const int64_t nqb = cdiv(query_tokens, SOL_BLOCK);
+  if (nkb > SOL_MAX_KEY_BLOCKS)
+    return fail(SOL_ERR_UNSUPPORTED, "sol_attention_fwd: key_tokens exceeds 64 * SOL_MAX_KEY_BLOCKS");
+  if (batch * heads * nqb >= (int64_t(1) << 31))
+    return fail(SOL_ERR_UNSUPPORTED, "sol_attention_fwd: grid too large");
+  sol::AttnParams p;
+  p.q = rows_of(q, q_strides, query_index, query_tokens);
+  p.k = rows_of(k, k_strides, key_index, key_tokens);
+  p.v = rows_of(v, v_strides, key_index, key_tokens);
+  p.kc = static_cast<const uint16_t*>(kc);
+  p.vct = static_cast<const uint16_t*>(vct);
+  p.mean = key_mean;
+  p.var = key_var;
+  p.protection = protection;
+  p.out = static_cast<uint16_t*>(out);
+  p.counts = counts;
+  p.dbg_selected = debug_selected;
+  p.dbg_proxy = debug_proxy;
+  p.dbg_cutoff = debug_cutoff;
+  p.B = int(batch);
+  p.H = int(heads);
+  p.Tq = int(query_tokens);
+  p.Tk = int(key_tokens);
+  p.NQB = int(nqb);
+  p.NKB = int(nkb);
+  p.NKBP = int(cdiv(nkb, 32) * 32);
+  p.scale = float(scale);
+  p.scale_log2 = float(scale * 1.4426950408889634);
+  p.beta = force == 0 ? float(beta) : 0.f;
+  p.force = force;
+  const int64_t big = int64_t(1) << 30;
+  p.local_blocks = int(local_blocks < 0 ? -1 : (local_blocks > big ? big : local_blocks));
+  p.kv_sink_blocks = int(cdiv(kv_sink_tokens > big ? big : kv_sink_tokens, SOL_BLOCK));
+  p.q_sink_blocks = int(cdiv(query_sink_tokens > big ? big : query_sink_tokens, SOL_BLOCK));
+  return hip_status(sol::launch_sol(p, int(head_dim), static_cast<hipStream_t>(stream)));
+}
+
+int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
+                  const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                  int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                  int64_t head_dim, double scale, void* out, void* stream) {
+  if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
+      key_tokens >= (int64_t(1) << 30))
+    return fail(SOL_ERR_INVALID, "sol_dense_fwd: unsupported shape (head_dim must be 64 or 128)");
+  if (!operand_ok(q, q_strides, false) || !operand_ok(k, k_strides, false) ||
+      !operand_ok(v, v_strides, false))
+    return fail(SOL_ERR_INVALID, "sol_dense_fwd: Q/K/V need 16-byte aligned rows and positive strides");
+  if (!std::isfinite(scale) || scale <= 0)
+    return fail(SOL_ERR_INVALID, "sol_dense_fwd: scale must be finite and positive");
+  if (!out || !aligned16(out)) return fail(SOL_ERR_INVALID, "sol_dense_fwd: out must be 16-byte aligned");
+  if (batch * heads * cdiv(query_tokens, 128) >= (int64_t(1) << 31))
+    return fail(SOL_ERR_UNSUPPORTED, "sol_dense_fwd: grid too large");
+  sol::AttnParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = rows_of(q, q_strides, nullptr, query_tokens);
+  p.k = rows_of(k, k_strides, nullptr, key_tokens);
+  p.v = rows_of(v, v_strides, nullptr, key_tokens);
+  p.out = static_cast<uint16_t*>(out);
+  p.B = int(batch);
+  p.H = int(heads);
+  p.Tq = int(query_tokens);
+  p.Tk = int(key_tokens);
+  p.NQB = int(cdiv(query_tokens, SOL_BLOCK));
+  p.NKB = int(cdiv(key_tokens, SOL_BLOCK));
+  p.scale = float(scale);
+  p.scale_log2 = float(scale * 1.4426950408889634);
+  return hip_status(sol::launch_dense(p, int(head_dim), static_cast<hipStream_t>(stream)));
+}
+
+}  // extern "C"

@@ -1,0 +1,162 @@
+// K/V block pooling and diagonal key moments for SOL routed attention.
+//
+// Replaces the reference's `_pool` + `_pooled` (src/sol_attn_amd/kernels.py:16-27,
+// 185-190) and `_moments` (kernels.py:30-49).  HBM-bound: every K and V token
+// row is read exactly once with 16-byte loads; centroids are written in the
+// layouts the attention kernel consumes:
+//   KC  [B, H, NKB, D]   bf16, one contiguous row per key block
+//   VCt [B, H, D, NKBP]  bf16, key blocks contiguous per feature (NKBP = NKB
+//                        rounded up to 32, zero padded) -> MFMA A operand
+// Sums follow torch's CPU outer-reduction order (16-row sequential chunks,
+// folded in order), so the FP32 means and the BF16-rounded centroids equal the
+// reference oracle's `x[:, i:i+64].float().mean(1)` bit for bit.
+#include "sol_device.h"
+#include "sol_internal.h"
+
+// This file is compiled with -ffp-contract=off: every product and sum below is
+// rounded on its own, as in torch's CPU reduction (a fused sq - m*m would
+// differ in the last bit).
+
+namespace sol {
+
+template <int D>
+__global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
+  constexpr int DC = D / 8;          // 16-byte chunks per token row
+  constexpr int LPB = DC * 4;        // lanes per key block: 4 chunks of 16 rows
+  constexpr int BPI = kWave / LPB;   // key blocks per wave iteration
+  __shared__ __align__(16) uint16_t cent[kPoolChunk][D];
+
+  const bool is_v = blockIdx.y != 0;
+  const TokenRows src = is_v ? p.v : p.k;
+  const int c = blockIdx.x % p.NCHP;
+  const int bh = blockIdx.x / p.NCHP;
+  const int h = bh % p.H, b = bh / p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int sub = lane / LPB, r4 = (lane % LPB) / DC, dc = lane % DC;
+
+#pragma unroll
+  for (int it = 0; it < 4 / BPI; ++it) {
+    const int jb = wave * 4 + it * BPI + sub;  // block inside this chunk
+    const int j = c * kPoolChunk + jb;
+    float s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = 0.f;
+    int len = 0;
+    if (j < p.NKB) {
+      len = min(kBlock, p.Tk - kBlock * j);
+      u32x4 x[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = 16 * r4 + i;
+        x[i] = t < len ? load16(src.row(b, kBlock * j + t, h) + 8 * dc) : zero_u32x4();
+      }
+      // Sequential accumulation inside the 16-row chunk (torch order).
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (16 * r4 + i < len) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t w = x[i][e >> 1];
+            s[e] = __fadd_rn(s[e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)));
+          }
+        }
+      }
+    }
+    float t1[8], t2[8], t3[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      t1[e] = __shfl(s[e], lane + DC);
+      t2[e] = __shfl(s[e], lane + 2 * DC);
+      t3[e] = __shfl(s[e], lane + 3 * DC);
+    }
+    if (r4 == 0) {
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float m0 = 0.f, m1 = 0.f;
+        if (len > 0) {
+          const float a0 = __fadd_rn(__fadd_rn(__fadd_rn(s[e], t1[e]), t2[e]), t3[e]);
+          const float a1 = __fadd_rn(__fadd_rn(__fadd_rn(s[e + 1], t1[e + 1]), t2[e + 1]), t3[e + 1]);
+          m0 = __fdiv_rn(a0, float(len));
+          m1 = __fdiv_rn(a1, float(len));
+        }
+        o[e >> 1] = pack_bf16x2(m0, m1);
+      }
+      *reinterpret_cast<u32x4*>(&cent[jb][8 * dc]) = o;
+    }
+  }
+  __syncthreads();
+
+  const int64_t head = int64_t(b) * p.H + h;
+  if (!is_v) {
+    if (tid < kPoolChunk * DC) {
+      const int jb = tid / DC, cc = tid % DC;
+      const int j = c * kPoolChunk + jb;
+      if (j < p.NKB)
+        *reinterpret_cast<u32x4*>(p.kc + (head * p.NKB + j) * D + 8 * cc) =
+            *reinterpret_cast<const u32x4*>(&cent[jb][8 * cc]);
+    }
+    // Chunk partial sums of the BF16 centroids and their squares (moments).
+    const int nch = (p.NKB + kPoolChunk - 1) / kPoolChunk;
+    if (p.ksum && c < nch && tid < D) {
+      const int rows = min(kPoolChunk, p.NKB - c * kPoolChunk);
+      float s1 = 0.f, s2 = 0.f;
+      for (int jb = 0; jb < rows; ++jb) {
+        const float x = bf16_bits_to_f32(cent[jb][tid]);
+        s1 = __fadd_rn(s1, x);
+        s2 = __fadd_rn(s2, __fmul_rn(x, x));
+      }
+      float* dst = p.ksum + ((head * nch + c) * 2) * D;
+      dst[tid] = s1;
+      dst[D + tid] = s2;
+    }
+  } else if (tid < 2 * D) {
+    const int d = tid >> 1, half = tid & 1;
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = uint32_t(cent[8 * half + 2 * e][d]) | (uint32_t(cent[8 * half + 2 * e + 1][d]) << 16);
+    *reinterpret_cast<u32x4*>(p.vct + (head * D + d) * p.NKBP + c * kPoolChunk + 8 * half) = o;
+  }
+}
+
+// One workgroup per (batch, head): fold the chunk sums in torch's cascade order.
+template <int D>
+__global__ __launch_bounds__(D) void moments_kernel(const float* __restrict__ ksum,
+                                                    float* __restrict__ mean,
+                                                    float* __restrict__ var, int nkb) {
+  const int bh = blockIdx.x, d = threadIdx.x;
+  const int nch = (nkb + kPoolChunk - 1) / kPoolChunk;
+  const float* base = ksum + int64_t(bh) * nch * 2 * D;
+  CascadeFold f1, f2;
+  for (int c = 0; c < nch; ++c) {
+    const int rows = min(kPoolChunk, nkb - c * kPoolChunk);
+    f1.push(base[(2 * c) * D + d], rows);
+    f2.push(base[(2 * c + 1) * D + d], rows);
+  }
+  const float n = float(nkb);
+  const float m = __fdiv_rn(f1.total(), n);
+  const float sq = __fdiv_rn(f2.total(), n);
+  const float v = __fsub_rn(sq, __fmul_rn(m, m));
+  mean[int64_t(bh) * D + d] = m;
+  var[int64_t(bh) * D + d] = v > 0.f ? v : 0.f;
+}
+
+hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
+  const dim3 grid(unsigned(p.B) * p.H * p.NCHP, 2);
+  if (D == 128)
+    hipLaunchKernelGGL(pool_kv_kernel<128>, grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(pool_kv_kernel<64>, grid, dim3(256), 0, stream, p);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || !p.ksum) return err;
+  if (D == 128)
+    hipLaunchKernelGGL(moments_kernel<128>, dim3(p.B * p.H), dim3(128), 0, stream,
+                       p.ksum, p.mean, p.var, p.NKB);
+  else
+    hipLaunchKernelGGL(moments_kernel<64>, dim3(p.B * p.H), dim3(64), 0, stream,
+                       p.ksum, p.mean, p.var, p.NKB);
+  return hipGetLastError();
+}
+
+}  // namespace sol

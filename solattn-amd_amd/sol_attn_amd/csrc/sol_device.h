@@ -1,0 +1,130 @@
+// Device-side building blocks shared by the SOL routed-attention kernels.
+//
+// Target: gfx950 (CDNA4), 64-wide wavefronts, bf16 MFMA 32x32x16.
+//
+// Matrix-core conventions used throughout (v_mfma_f32_32x32x16_bf16):
+//   A operand (32 x 16): lane l supplies row (l % 32), k-slots 8*(l/32) .. +7
+//   B operand (16 x 32): lane l supplies column (l % 32), k-slots 8*(l/32) .. +7
+//   C/D (32 x 32):       lane l holds column (l % 32); element e holds row
+//                        8*(e/4) + 4*(l/32) + (e%4)
+// Scores are computed transposed, S^T = K * Q^T, so each lane owns ONE query
+// (its C column) and the softmax row statistics never leave the lane pair
+// (l, l ^ 32).  P^T then feeds O^T = V^T * P^T as the B operand straight
+// from registers; only V needs a transposed (key-contiguous) LDS tile.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sol {
+
+constexpr int kBlock = 64;      // tokens per physical block (kernels.py:12)
+constexpr int kWave = 64;       // CDNA wavefront width
+constexpr int kMaxKeyBlocks = 8192;  // LDS routing bitmask capacity (Tk <= 524288)
+constexpr int kPoolChunk = 16;  // key blocks per pooling workgroup (= cascade chunk)
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+// Round-to-nearest-even float -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  __bf16 h = static_cast<__bf16>(f);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
+}
+
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 u) { return __builtin_bit_cast(bf16x8, u); }
+
+__device__ __forceinline__ u32x4 zero_u32x4() {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return z;
+}
+
+// Row of one attention operand: token t of batch b, head h.  Either strided
+// BTHD addressing or (indexed windows) a gather through an int64 token index.
+struct TokenRows {
+  const uint16_t* base;
+  const int64_t* index;  // nullable; [B, T] original token ids
+  int64_t sb, st, sh;    // element strides (batch ignored when indexed)
+  int T;
+
+  __device__ __forceinline__ const uint16_t* row(int b, int t, int h) const {
+    if (index) return base + index[int64_t(b) * T + t] * st + int64_t(h) * sh;
+    return base + int64_t(b) * sb + int64_t(t) * st + int64_t(h) * sh;
+  }
+};
+
+__device__ __forceinline__ u32x4 load16(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ u32x2 load8(const uint16_t* p) {
+  return *reinterpret_cast<const u32x2*>(p);
+}
+
+// 8x8 bf16 transpose of eight 16-byte rows: out[d] packs rows 0..7 of column d.
+__device__ __forceinline__ void transpose8x8(const u32x4 (&in)[8], u32x4 (&out)[8]) {
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+#pragma unroll
+    for (int kp = 0; kp < 4; ++kp) {
+      const uint32_t lo = in[2 * kp][d / 2];
+      const uint32_t hi = in[2 * kp + 1][d / 2];
+      out[d][kp] = (d & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u))
+                           : ((lo & 0xFFFFu) | (hi << 16));
+    }
+  }
+}
+
+// Torch-order fold of a block-axis reduction made of 16-row chunk sums.
+// Chunk sums arrive in order; full chunks cascade through three levels
+// (carry every 16 rows, again every 256, again every 4096); a trailing partial
+// chunk is added first at the end: ((rem + a1) + a2) + a3.
+struct CascadeFold {
+  float a1 = 0.f, a2 = 0.f, a3 = 0.f, rem = 0.f;
+  int rows = 0;
+  __device__ __forceinline__ void push(float chunk_sum, int chunk_rows) {
+    if (chunk_rows == 16) {
+      rows += 16;
+      a1 = __fadd_rn(a1, chunk_sum);
+      if ((rows & 0xF0) == 0) {
+        a2 = __fadd_rn(a2, a1);
+        a1 = 0.f;
+        if ((rows & 0xF00) == 0) {
+          a3 = __fadd_rn(a3, a2);
+          a2 = 0.f;
+        }
+      }
+    } else {
+      rem = chunk_sum;
+    }
+  }
+  __device__ __forceinline__ float total() const {
+    return __fadd_rn(__fadd_rn(__fadd_rn(rem, a1), a2), a3);
+  }
+};
+
+}  // namespace sol

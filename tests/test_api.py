@@ -1,0 +1,154 @@
+"""CPU tests of the host contract: validation, plan builder, C-ABI exports."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from sol_attn_amd import IndexedPlan, SolStats, dense_attention, sol_attention, sol_attention_indexed
+from sol_attn_amd import _native
+from sol_testlib import tensors
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sol_attn_amd.h")
+
+
+def test_api_rejects_unsupported_input():
+    # test_attention.py:149-156 (dtype and grad checks precede the device check)
+    q, k, v = tensors()
+    with pytest.raises(ValueError, match="AMD ROCm GPU"):
+        sol_attention(q, k, v)
+    with pytest.raises(ValueError, match="Only BF16"):
+        sol_attention(q.float(), k.float(), v.float())
+    with pytest.raises(ValueError, match="Inference only"):
+        sol_attention(q.requires_grad_(), k, v)
+
+
+@pytest.mark.parametrize("bad,match", [
+    (lambda q, k, v: (q[0], k, v), "BTHD rank-4"),
+    (lambda q, k, v: (q, k[:, :, :1], v), "must agree and be nonempty"),
+    (lambda q, k, v: (q[..., :32], k[..., :32], v[..., :32]), "head dimensions 64 and 128"),
+    (lambda q, k, v: (q.transpose(2, 3), k, v), None),
+])
+def test_api_validation_messages(bad, match):
+    q, k, v = tensors()
+    args = bad(q, k, v)
+    with pytest.raises(ValueError, match=match):
+        sol_attention(*args)
+    with pytest.raises(ValueError, match=match):
+        dense_attention(*args)
+
+
+def test_api_keyword_only_and_no_masks():
+    q, k, v = tensors()
+    with pytest.raises(TypeError):
+        sol_attention(q, k, v, 1.0)
+    with pytest.raises(TypeError):
+        sol_attention(q, k, v, attn_mask=None)
+    with pytest.raises(TypeError):
+        sol_attention_indexed(q[0], k[0], v[0], None, 1.0)
+
+
+@pytest.mark.parametrize("kind", ["unsorted", "duplicate", "negative", "outside", "dtype", "batch"])
+def test_indexed_rejects_invalid_metadata(kind):
+    # test_indexed.py:45-56
+    rows = torch.tensor([[1, 2]], dtype=torch.int64)
+    keys = torch.arange(8).reshape(1, -1)
+    if kind == "unsorted": keys = keys.flip(1)
+    if kind == "duplicate": keys[0, 1] = 0
+    if kind == "negative": rows[0, 0] = -1
+    if kind == "outside": keys[0, -1] = 20
+    if kind == "dtype": keys = keys.int()
+    if kind == "batch": rows = rows.repeat(2, 1)
+    with pytest.raises(ValueError):
+        IndexedPlan.create(rows, keys, 20)
+
+
+def test_indexed_protection_uses_original_indices():
+    # test_indexed.py:20-29
+    rows = torch.stack((torch.arange(87, 152), torch.arange(300, 365)))
+    keys = torch.stack((torch.cat((torch.arange(0, 23), torch.arange(70, 198), torch.arange(500, 509))),
+                        torch.cat((torch.arange(0, 23), torch.arange(283, 411), torch.arange(500, 509)))))
+    p = IndexedPlan.create(rows, keys, 509, protected_ranges=((0, 23), (500, 509)), local_tokens=0)
+    assert p.protected_blocks.shape == (2, 2, 3)
+    assert p.protected_blocks.all()
+    p = IndexedPlan.create(torch.tensor([[400]], dtype=torch.int64), torch.arange(128).reshape(1, -1),
+                           509, local_tokens=0)
+    assert not p.protected_blocks.any()
+
+
+def test_indexed_plan_matches_oracle_on_random_windows():
+    from oracle.sol_oracle import plan_protection
+    rng = np.random.default_rng(12)
+    for trial in range(20):
+        w, seq = int(rng.integers(1, 4)), int(rng.integers(200, 3000))
+        nq, nk = int(rng.integers(1, min(seq, 300))), int(rng.integers(1, min(seq, 400)))
+        rows = np.stack([np.sort(rng.choice(seq, nq, replace=False)) for _ in range(w)])
+        keys = np.stack([np.sort(rng.choice(seq, nk, replace=False)) for _ in range(w)])
+        a = int(rng.integers(0, seq - 1))
+        ranges = ((a, int(rng.integers(a + 1, seq + 1))),)
+        local = int(rng.integers(0, 100))
+        p = IndexedPlan.create(torch.from_numpy(rows), torch.from_numpy(keys), seq,
+                               protected_ranges=ranges, local_tokens=local)
+        np.testing.assert_array_equal(p.protected_blocks.numpy(),
+                                      plan_protection(rows, keys, seq, ranges, local))
+
+
+def test_indexed_api_rejects_cpu_inputs():
+    p = IndexedPlan.create(torch.tensor([[1, 2]]), torch.arange(8).reshape(1, -1), 20)
+    x = torch.randn((20, 2, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="AMD ROCm GPU"):
+        sol_attention_indexed(x, x, x, p)
+    with pytest.raises(ValueError, match="matching NHD"):
+        sol_attention_indexed(x, x[:10], x, p)
+
+
+def test_stats_density():
+    s = SolStats(torch.tensor([[[2, 4]]], dtype=torch.int32), 4)
+    assert s.density() == 0.75
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(sol_\w+)\(", text, re.M)))
+
+
+def test_c_abi_library_exports_every_declared_symbol():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("libsol_attn_amd.so not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    names = _declared_functions()
+    assert set(names) >= {"sol_abi_version", "sol_last_error", "sol_pool_kv", "sol_attention_fwd",
+                          "sol_dense_fwd", "sol_pool_sizes"}
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_native._SIGNATURES)
+    native = _native.library()
+    assert native.sol_abi_version() == 1
+    sizes = (ctypes.c_int64 * 4)()
+    assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
+    assert list(sizes) == [1 * 2 * 5 * 64 * 2, 1 * 2 * 64 * 32 * 2, 1 * 2 * 1 * 2 * 64 * 4, 2 * 64 * 4]
+    assert native.sol_pool_sizes(1, 317, 2, 96, sizes) == -1
+    assert b"invalid shape" in native.sol_last_error()
+
+
+def test_c_abi_rejects_bad_arguments_without_launching():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("libsol_attn_amd.so not built")
+    native = _native.library()
+    strides = (ctypes.c_int64 * 3)(64 * 2 * 317, 128, 64)
+    fake = ctypes.c_void_p(1 << 20)   # never dereferenced: validation fails first
+    rc = native.sol_dense_fwd(fake, strides, fake, strides, fake, strides, 1, 193, 317, 2, 64,
+                              float("nan"), fake, None)
+    assert rc == -1 and b"scale" in native.sol_last_error()
+    rc = native.sol_attention_fwd(fake, strides, None, fake, strides, fake, strides, None,
+                                  1, 193, 317, 2, 64, fake, fake, None, None, None,
+                                  0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None)
+    assert rc == -1 and b"key_mean" in native.sol_last_error()
+    bad = (ctypes.c_int64 * 3)(64 * 2 * 317, 127, 64)
+    rc = native.sol_pool_kv(fake, bad, fake, strides, None, 1, 317, 2, 64, fake, fake,
+                            None, None, None, None)
+    assert rc == -1 and b"aligned" in native.sol_last_error()

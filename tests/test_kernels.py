@@ -1,0 +1,164 @@
+"""GPU kernel-level parity: pooling bit-exactness, routing decisions within the
+stated band, outputs under identical routing, and the dense limit.
+
+Routing band (stated here and used by every decision check): a kernel decision
+may differ from the oracle's only for blocks with
+``|proxy - cutoff| <= 1e-5 * max(|cutoff|, scale * |Qc| * |Kc_j|)``
+(oracle values, natural-log units); ``|.|`` are Euclidean norms.  The second
+term is the magnitude the FP32 proxy dot product is rounded against.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sol_oracle as orc
+from sol_attn_amd import _native, dense_attention, sol_attention
+from sol_testlib import HAS_GPU, assert_close, block_smooth, tensors, to_np
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not HAS_GPU, reason="AMD ROCm GPU required")]
+
+BAND = 1e-5
+
+
+def kernel_pool(k, v, moments=True):
+    with torch.no_grad():
+        return _native.pool_kv(k, v, moments=moments)
+
+
+@pytest.mark.parametrize("shape", [(1, 317, 2, 64), (2, 1089, 3, 128), (1, 1, 1, 64), (2, 4096, 16, 128),
+                                   (1, 10000, 4, 128)])
+def test_pooling_and_moments_bit_exact(shape):
+    b, t, h, d = shape
+    g = torch.Generator().manual_seed(t)
+    k = torch.randn(shape, generator=g, dtype=torch.bfloat16)
+    v = torch.randn(shape, generator=g, dtype=torch.bfloat16)
+    out = kernel_pool(k.cuda(), v.cuda())
+    torch.cuda.synchronize()
+    kc = orc.block_means(to_np(k), True)          # [B, NKB, H, D]
+    vc = orc.block_means(to_np(v), True)
+    mean, var = orc.key_moments(kc)
+    nkb = kc.shape[1]
+    np.testing.assert_array_equal(to_np(out["kc"]).transpose(0, 2, 1, 3), kc)
+    vct = to_np(out["vct"])
+    np.testing.assert_array_equal(vct[..., :nkb].transpose(0, 3, 1, 2), vc)
+    assert (vct[..., nkb:] == 0).all()
+    np.testing.assert_array_equal(to_np(out["mean"]), mean)
+    np.testing.assert_array_equal(to_np(out["var"]), var)
+
+
+def test_pooling_strided_and_indexed_gather():
+    g = torch.Generator().manual_seed(9)
+    base = torch.randn((900, 6, 64), generator=g, dtype=torch.bfloat16)
+    keys = torch.stack((torch.arange(3, 503), torch.arange(350, 850)))
+    k = base.cuda()[:, ::2]                     # NHD, head stride 128 elements
+    v = (base.cuda() * 2)[:, 1::2]
+    out = _native.pool_kv(k, v, key_index=keys.cuda())
+    kc = orc.block_means(to_np(k.cpu()[keys]), True)
+    vc = orc.block_means(to_np(v.cpu()[keys]), True)
+    np.testing.assert_array_equal(to_np(out["kc"]).transpose(0, 2, 1, 3), kc)
+    np.testing.assert_array_equal(to_np(out["vct"])[..., :kc.shape[1]].transpose(0, 3, 1, 2), vc)
+    mean, var = orc.key_moments(kc)
+    np.testing.assert_array_equal(to_np(out["mean"]), mean)
+    np.testing.assert_array_equal(to_np(out["var"]), var)
+
+
+def run_debug(q, k, v, beta, scale=None, local=1, kv_sink=0, q_sink=0):
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    with torch.no_grad():
+        out, counts, dbg = _native.launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, True,
+                                              debug=True)
+    torch.cuda.synchronize()
+    return out, counts, dbg
+
+
+def check_routing(q, k, v, beta, scale=None, local=1, kv_sink=0, q_sink=0, query_blocks=None,
+                  max_band_mismatch=None):
+    """Decisions vs oracle (band), outputs under identical routing, counts.
+
+    Returns ``(kernel_out, oracle_out_under_kernel_routing, qrows)``."""
+    qn, kn, vn = to_np(q.cpu()), to_np(k.cpu()), to_np(v.cpu())
+    d = qn.shape[-1]
+    s = d ** -0.5 if scale is None else scale
+    out, counts, dbg = run_debug(q, k, v, beta, s, local, kv_sink, q_sink)
+    qm = orc.block_means(qn, False)
+    kc = orc.block_means(kn, True)
+    mean, var = orc.key_moments(kc)
+    cut = orc.cutoffs(qm, mean, var, beta, s)
+    sel, proxy = orc.route(qn, kc, cut, beta=beta, scale=s, local_blocks=local,
+                           kv_sink_tokens=kv_sink, query_sink_tokens=q_sink, query_blocks=query_blocks)
+    ksel = to_np(dbg["selected"]).astype(bool)
+    qbs = np.arange(qm.shape[1]) if query_blocks is None else np.asarray(query_blocks)
+    ksel_s, sel_s = ksel[:, qbs], sel[:, qbs]
+    mismatch = ksel_s != sel_s
+    if mismatch.any():
+        assert math.isfinite(beta), "infinite beta routing must match exactly"
+        c = cut[:, qbs][..., None]
+        qn_norm = np.linalg.norm(qm[:, qbs], axis=-1)[..., None]            # [B, n, H, 1]
+        kn_norm = np.linalg.norm(kc, axis=-1).transpose(0, 2, 1)[:, None]   # [B, 1, H, NKB]
+        band = BAND * np.maximum(np.abs(c), s * qn_norm * kn_norm)
+        gap = np.abs(proxy[:, qbs] - c)
+        outside = mismatch & (gap > band)
+        assert not outside.any(), f"{int(outside.sum())} routing decisions differ outside the band"
+        if max_band_mismatch is not None:
+            assert mismatch.sum() <= max_band_mismatch
+    # Kernel proxies and cutoffs agree with the oracle's to FP32 rounding.
+    if math.isfinite(beta):
+        kp = to_np(dbg["proxy"])[:, qbs]
+        np.testing.assert_allclose(kp, proxy[:, qbs], rtol=1e-4, atol=1e-5 * np.abs(proxy[:, qbs]).max())
+        np.testing.assert_allclose(to_np(dbg["cutoff"])[:, qbs], cut[:, qbs], rtol=1e-4,
+                                   atol=1e-5 * np.abs(cut).max())
+    kcounts = counts.cpu().numpy()[:, qbs]
+    np.testing.assert_array_equal(kcounts, ksel_s.sum(-1))
+    # (b) output under identical routing: the oracle evaluated with the kernel's decisions.
+    ref, _, _ = orc.sol_oracle(qn, kn, vn, beta=beta, scale=s, local_blocks=local,
+                               kv_sink_tokens=kv_sink, query_sink_tokens=q_sink,
+                               query_blocks=list(qbs), selected=ksel)
+    rows = np.concatenate([np.arange(64 * x, min(qn.shape[1], 64 * x + 64)) for x in qbs])
+    return to_np(out.cpu())[:, rows], ref[:, rows], mismatch
+
+
+@pytest.mark.parametrize("beta", [-math.inf, 0.0, 1.0, math.inf])
+@pytest.mark.parametrize("kind", ["smooth", "random"])
+def test_c2_shape_routing_and_output(beta, kind):
+    # B=2, T=4096, H=16, D=128, sinks 128, local 1; oracle on 6 query blocks.
+    if kind == "smooth":
+        q, k, v = (block_smooth(2, 4096, 16, 128, seed=s, device="cuda") for s in (1, 2, 3))
+    else:
+        q, k, v = tensors(nq=4096, nk=4096, d=128, b=2, h=16, device="cuda", seed=0)
+    qbs = [0, 1, 2, 31, 32, 63]
+    actual, ref, _ = check_routing(q, k, v, beta, kv_sink=128, q_sink=128, query_blocks=qbs)
+    assert_close(actual, ref)
+
+
+def test_c3_ragged_cross_attention_strided_query():
+    # B=1, H=24, D=128, Tq=4096, Tk=10000, Q head-strided view, random; beta 1,
+    # kv sink 64, q sink 0, local 0.
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn((1, 4096, 48, 128), generator=g, device="cuda", dtype=torch.bfloat16)[:, :, ::2]
+    k = torch.randn((1, 10000, 24, 128), generator=g, device="cuda", dtype=torch.bfloat16)
+    v = torch.randn((1, 10000, 24, 128), generator=g, device="cuda", dtype=torch.bfloat16)
+    actual, ref, _ = check_routing(q, k, v, 1.0, local=0, kv_sink=64, q_sink=0,
+                                   query_blocks=[0, 17, 40, 63])
+    assert_close(actual, ref)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_dense_limit_matches_dense_kernel(d):
+    # (c) beta=-inf reproduces dense attention within BF16 tolerance.
+    q, k, v = tensors(nq=777, nk=1500, d=d, b=2, h=3, device="cuda", seed=4)
+    sol = sol_attention(q, k, v, beta=-math.inf)
+    dense = dense_attention(q, k, v)
+    assert_close(sol.cpu(), dense.cpu())
+    assert_close(dense.cpu(), orc.dense_oracle(q.cpu(), k.cpu(), v.cpu()))
+
+
+def test_repeat_calls_are_bitwise_deterministic():
+    q, k, v = (block_smooth(1, 3000, 8, 128, seed=s, device="cuda") for s in (5, 6, 7))
+    a, sa = sol_attention(q, k, v, beta=1.0, kv_sink_tokens=128, query_sink_tokens=128, return_stats=True)
+    for _ in range(3):
+        b, sb = sol_attention(q, k, v, beta=1.0, kv_sink_tokens=128, query_sink_tokens=128,
+                              return_stats=True)
+        assert torch.equal(a, b) and torch.equal(sa.exact_blocks, sb.exact_blocks)
