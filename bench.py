@@ -1,0 +1,239 @@
+"""SOL routed attention benchmark on one MI355X.
+
+Workload (default): Video-DiT-shaped self-attention, B=1, 21 x 48 x 84 =
+84,672 tokens, H=24, D=128, BF16, spatiotemporally smooth Q/K/V field (per
+head a N(0,1) grid of 6 x 12 x 21 x 128 over (frame, h, w), trilinearly
+upsampled, plus 0.2 * N(0,1) per-token noise), beta=1, kv/query sinks 128,
+local_blocks=1.  A step is one all-in ``sol_attention`` call (pooling,
+moments, routing, attention, output allocation) with inputs resident in HBM.
+
+Prints ONE JSON line: ms/call, dense-equivalent TFLOP/s (4 B H Tq Tk D / t),
+density, the in-house dense HIP kernel, roofline of the dominant kernel
+(fused routing+attention, MFMA-bound) and of pooling (HBM-bound), parity
+against the oracle on sampled query blocks, and the oracle's CPU time on that
+sample (extrapolated to the full call).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "solattn-amd_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+import torch.nn.functional as F  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+WORKLOADS = {
+    "videodit-84672": dict(batch=1, frames=21, height=48, width=84, heads=24, head_dim=128,
+                           beta=1.0, kv_sink_tokens=128, query_sink_tokens=128, local_blocks=1,
+                           fixture="smooth-field", seed=0),
+    "selfattn-4096-smooth": dict(batch=2, tokens=4096, heads=16, head_dim=128, beta=1.0,
+                                 kv_sink_tokens=128, query_sink_tokens=128, local_blocks=1,
+                                 fixture="block-smooth", seed=0),
+    "selfattn-1024-smooth": dict(batch=1, tokens=1024, heads=8, head_dim=64, beta=1.0,
+                                 kv_sink_tokens=128, query_sink_tokens=128, local_blocks=1,
+                                 fixture="block-smooth", seed=0),
+}
+
+
+def smooth_field(gen, frames, height, width, heads, dim, device):
+    """Per head: N(0,1) grid [dim, 6, 12, 21] -> trilinear (frames, height, width) + 0.2 N(0,1)."""
+    grid = torch.randn((heads, dim, 6, 12, 21), generator=gen, device=device)
+    up = F.interpolate(grid, size=(frames, height, width), mode="trilinear", align_corners=False)
+    tokens = up.permute(2, 3, 4, 0, 1).reshape(1, frames * height * width, heads, dim).contiguous()
+    del up
+    noise = torch.randn(tokens.shape, generator=gen, device=device)
+    return (tokens + 0.2 * noise).to(torch.bfloat16).contiguous()
+
+
+def block_smooth(gen, batch, tokens, heads, dim, device, noise=0.1):
+    nb = (tokens + 63) // 64
+    centres = torch.randn((batch, nb, heads, dim), generator=gen, device=device)
+    x = centres.repeat_interleave(64, 1)[:, :tokens]
+    return (x + noise * torch.randn(x.shape, generator=gen, device=device)).to(torch.bfloat16)
+
+
+def make_inputs(cfg, device):
+    gen = torch.Generator(device=device).manual_seed(cfg["seed"])
+    if cfg["fixture"] == "smooth-field":
+        return [smooth_field(gen, cfg["frames"], cfg["height"], cfg["width"], cfg["heads"],
+                             cfg["head_dim"], device) for _ in range(3)]
+    return [block_smooth(gen, cfg["batch"], cfg["tokens"], cfg["heads"], cfg["head_dim"], device)
+            for _ in range(3)]
+
+
+def event_ms(fn, reps):
+    """Average ms per call of fn() on the current stream (HIP events)."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def routing_flops(selected, tq, tk, d):
+    """Algorithmic MFMA FLOPs of the fused kernel from its decision mask.
+
+    exact: 4 * qlen * klen * D per selected block; centroid path: 4 * qlen * D
+    per unselected block (score + weighted value)."""
+    sel = selected.to(torch.float64)                       # [B, NQB, H, NKB]
+    nqb, nkb = sel.shape[1], sel.shape[3]
+    qlen = torch.clamp(tq - 64 * torch.arange(nqb, dtype=torch.float64, device=sel.device), max=64)
+    klen = torch.clamp(tk - 64 * torch.arange(nkb, dtype=torch.float64, device=sel.device), max=64)
+    exact = 4.0 * d * torch.einsum("bqhk,q,k->", sel, qlen, klen).item()
+    approx = 4.0 * d * torch.einsum("bqhk,q->", 1.0 - sel, qlen).item()
+    return exact, approx
+
+
+def cpu_baseline(q, k, v, cfg, scale, sample, gpu_out, gpu_sel):
+    """The oracle on `sample` query blocks x all heads, timed on host cores."""
+    from oracle import sol_oracle as orc
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover - informational only
+        threads = os.cpu_count()
+    qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
+    kw = dict(beta=cfg["beta"], scale=scale, local_blocks=cfg["local_blocks"],
+              kv_sink_tokens=cfg["kv_sink_tokens"], query_sink_tokens=cfg["query_sink_tokens"])
+    t0 = time.perf_counter()
+    kc = orc.block_means(kn, True)
+    orc.block_means(vn, True)
+    orc.block_means(qn, False)
+    orc.key_moments(kc)
+    t_setup = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    out, counts, info = orc.sol_oracle(qn, kn, vn, query_blocks=sample, **kw)
+    t_sample = time.perf_counter() - t0
+    nqb = counts.shape[1]
+    per_block = max(t_sample - t_setup, 1e-9) / len(sample)
+    t_full = t_setup + per_block * nqb
+    rows = np.concatenate([np.arange(64 * x, min(qn.shape[1], 64 * x + 64)) for x in sample])
+    got = gpu_out[:, rows].float().cpu().numpy()
+    ref = out[:, rows]
+    ksel = gpu_sel[:, sample].cpu().numpy()
+    osel = info["selected"][:, sample]
+    parity = {"sampled_query_blocks": list(map(int, sample)),
+              "max_abs": float(np.abs(got - ref).max()),
+              "rel_l2": float(np.linalg.norm(got - ref) / np.linalg.norm(ref)),
+              "routing_decisions": int(osel.size),
+              "routing_mismatches": int((ksel != osel).sum()),
+              "counts_equal": bool(np.array_equal(ksel.sum(-1), counts[:, sample]))}
+    return t_full, t_sample, threads, parity
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="videodit-84672")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--dense-reps", type=int, default=2)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(heads would shard with no communication); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    from sol_attn_amd import _native, dense_attention, sol_attention
+
+    cfg = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q, k, v = make_inputs(cfg, dev)
+    b, t, h, d = q.shape
+    scale = d ** -0.5
+    kw = dict(beta=cfg["beta"], local_blocks=cfg["local_blocks"],
+              kv_sink_tokens=cfg["kv_sink_tokens"], query_sink_tokens=cfg["query_sink_tokens"])
+    dense_flops = 4.0 * b * h * t * t * d
+
+    def step():
+        return sol_attention(q, k, v, **kw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # Per-kernel breakdown with HIP events on the launch stream.
+    with torch.no_grad():
+        pooled = _native.pool_kv(k, v, moments=True)
+        pool_ms = event_ms(lambda: _native.pool_kv(k, v, moments=False), 10)
+        pool_mom_ms = event_ms(lambda: _native.pool_kv(k, v, moments=True), 10)
+        attn_ms = event_ms(lambda: _native.attend(q, k, v, pooled, scale, cfg["beta"],
+                                                  cfg["local_blocks"], cfg["kv_sink_tokens"],
+                                                  cfg["query_sink_tokens"]), max(3, args.steps // 2))
+        ref_out, counts, dbg = _native.attend(q, k, v, pooled, scale, cfg["beta"], cfg["local_blocks"],
+                                              cfg["kv_sink_tokens"], cfg["query_sink_tokens"],
+                                              debug=True)
+        dense_ms = event_ms(lambda: dense_attention(q, k, v), args.dense_reps)
+    torch.cuda.synchronize()
+    deterministic = bool(torch.equal(ref_out, out))
+    density = counts.float().mean().item() / dbg["selected"].shape[-1]
+    exact_flops, approx_flops = routing_flops(dbg["selected"], t, t, d)
+    attn_tflops = (exact_flops + approx_flops) / (attn_ms * 1e-3) / 1e12
+    pool_bytes = 2 * b * t * h * d * 2 + pooled["kc"].numel() * 2 + pooled["vct"].numel() * 2
+    pool_gbs = pool_bytes / (pool_ms * 1e-3) / 1e9
+
+    result = {
+        "metric": "ms/call & dense-equiv TFLOP/s at 84,672 tok H24 D128 BF16; density; err vs oracle",
+        "value": dense_flops / (wall_ms * 1e-3) / 1e12,
+        "unit": "dense-equiv TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall_ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": args.workload, "batch": b, "tokens": t, "heads": h, "head_dim": d,
+                   "beta": cfg["beta"], "kv_sink_tokens": cfg["kv_sink_tokens"],
+                   "query_sink_tokens": cfg["query_sink_tokens"], "local_blocks": cfg["local_blocks"],
+                   "fixture": cfg["fixture"], "seed": cfg["seed"]},
+        "density": density,
+        "deterministic_repeat": deterministic,
+        "kernels_ms": {"pool_kv": pool_ms, "pool_kv_moments": pool_mom_ms, "sol_attention": attn_ms,
+                       "dense_attention": dense_ms},
+        "dense_hip_ms": dense_ms,
+        "dense_hip_tflops": dense_flops / (dense_ms * 1e-3) / 1e12,
+        "speedup_vs_dense_hip": dense_ms / wall_ms,
+        "roofline": {"bound": "mfma", "achieved": attn_tflops, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": attn_tflops / PEAK_BF16_TFLOPS, "traffic": None,
+                     "kernel": "sol attention (routing + centroid correction + exact blocks)",
+                     "flops_per_launch": exact_flops + approx_flops, "exact_flops": exact_flops,
+                     "exact_only_frac": exact_flops / (attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
+        "pool_roofline": {"bound": "hbm", "achieved": pool_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": pool_gbs / PEAK_HBM_GBS, "bytes_per_launch": pool_bytes},
+    }
+    if not args.no_cpu:
+        nqb = (t + 63) // 64
+        sample = [0, nqb // 2, nqb - 1]
+        t_full, t_sample, threads, parity = cpu_baseline(q, k, v, cfg, scale, sample, out,
+                                                         dbg["selected"])
+        result["cpu_baseline"] = {
+            "value": dense_flops / t_full / 1e12, "unit": "dense-equiv TFLOP/s", "cores": threads,
+            "kind": "port", "ms_per_call_extrapolated": t_full * 1e3,
+            "sample": (f"oracle on query blocks {sample} x {h} heads (all keys, full pooling "
+                       f"and moments) in {t_sample:.1f} s; per-query-block cost extrapolated "
+                       f"to {nqb} blocks")}
+        result["parity_vs_oracle"] = parity
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -123,16 +123,14 @@ def pool_kv(k, v, key_index=None, moments=True):
     return {"kc": kc, "vct": vct, "mean": mean, "var": var}
 
 
-def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=None,
-               rows=None, keys=None, debug=False):
-    """All-in SOL attention (``kernels.py:203-225``): pooling, moments, routing, attention.
+def attend(q, k, v, pooled, scale, beta, local, kv_sink, q_sink, protection=None,
+           rows=None, keys=None, debug=False):
+    """Routing + attention over pooled keys (the ``_sol`` launch of ``kernels.py:218-224``).
 
-    ``rows``/``keys`` (indexed windows) gather Q and K/V token rows inside the
-    kernels instead of materialising copies.  Returns ``(out, counts)`` and,
-    with ``debug=True``, a dict of routing diagnostics as a third element.
+    ``pooled`` is the dict returned by :func:`pool_kv` for the same keys.
+    Returns ``(out, counts, dbg)``; ``dbg`` is None unless ``debug``.
     """
     lib = library()
-    finite = not math.isinf(beta)
     indexed = keys is not None
     if indexed:
         b, nq = rows.shape
@@ -144,7 +142,6 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
     q, k, v = _rows(q), _rows(k), _rows(v)
     dev = q.device
     nqb, nkb = -(-nq // BLOCK), -(-nk // BLOCK)
-    pooled = pool_kv(k, v, key_index=keys, moments=finite)
     out = torch.empty((b, nq, h, d), device=dev, dtype=torch.bfloat16)
     counts = torch.empty((b, nqb, h), device=dev, dtype=torch.int32)
     dbg = None
@@ -165,6 +162,21 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
         _stream(dev)))
     if debug:
         dbg["selected"] = dbg["selected"].bool()
+    return out, counts, dbg
+
+
+def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=None,
+               rows=None, keys=None, debug=False):
+    """All-in SOL attention (``kernels.py:203-225``): pooling, moments, routing, attention.
+
+    ``rows``/``keys`` (indexed windows) gather Q and K/V token rows inside the
+    kernels instead of materialising copies.  Returns ``(out, counts)`` and,
+    with ``debug=True``, a dict of routing diagnostics as a third element.
+    """
+    pooled = pool_kv(_rows(k), _rows(v), key_index=keys, moments=not math.isinf(beta))
+    out, counts, dbg = attend(q, k, v, pooled, scale, beta, local, kv_sink, q_sink,
+                              protection, rows, keys, debug)
+    if debug:
         dbg.update(pooled)
         return out, counts, dbg
     return out, counts
