@@ -179,10 +179,10 @@ def main():
         pooled = _native.pool_kv(k, v, moments=True)
         pool_ms = event_ms(lambda: _native.pool_kv(k, v, moments=False), 10)
         pool_mom_ms = event_ms(lambda: _native.pool_kv(k, v, moments=True), 10)
-        attn_ms = event_ms(lambda: _native.attend(q, k, v, pooled, scale, cfg["beta"],
-                                                  cfg["local_blocks"], cfg["kv_sink_tokens"],
-                                                  cfg["query_sink_tokens"]), max(3, args.steps // 2))
-        ref_out, counts, dbg = _native.attend(q, k, v, pooled, scale, cfg["beta"], cfg["local_blocks"],
+        attn_ms = event_ms(lambda: _native.attend(q, pooled, scale, cfg["beta"], cfg["local_blocks"],
+                                                  cfg["kv_sink_tokens"], cfg["query_sink_tokens"]),
+                           max(3, args.steps // 2))
+        ref_out, counts, dbg = _native.attend(q, pooled, scale, cfg["beta"], cfg["local_blocks"],
                                               cfg["kv_sink_tokens"], cfg["query_sink_tokens"],
                                               debug=True)
         dense_ms = event_ms(lambda: dense_attention(q, k, v), args.dense_reps)
@@ -191,7 +191,9 @@ def main():
     density = counts.float().mean().item() / dbg["selected"].shape[-1]
     exact_flops, approx_flops = routing_flops(dbg["selected"], t, t, d)
     attn_tflops = (exact_flops + approx_flops) / (attn_ms * 1e-3) / 1e12
-    pool_bytes = 2 * b * t * h * d * 2 + pooled["kc"].numel() * 2 + pooled["vct"].numel() * 2
+    # Algorithmic pooling bytes: read K and V once; write centroids and the K / V^T tiles.
+    pool_bytes = (2 * b * t * h * d * 2 + pooled["kc"].numel() * 2 + pooled["vct"].numel() * 2
+                  + pooled["tiles"].numel() * 2)
     pool_gbs = pool_bytes / (pool_ms * 1e-3) / 1e9
 
     result = {

@@ -51,24 +51,28 @@ const char* sol_last_error(void);
  *   sizes[1] vct         bf16 [batch, heads, head_dim, NKBP]  (NKBP = NKB rounded up to 32)
  *   sizes[2] chunk_sums  fp32 [batch, heads, ceil(NKB/16), 2, head_dim]
  *   sizes[3] key_mean    fp32 [batch, heads, head_dim]  (key_var has the same size)
+ *   sizes[4] tiles       bf16 [batch, heads, NKB, 2, 64 * head_dim]  K and V^T block tiles
  * with NKB = ceil(key_tokens / 64). */
 int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
-                   int64_t sizes[4]);
+                   int64_t sizes[5]);
 
-/* K/V block pooling and diagonal key moments.
+/* K/V block pooling, attention tiles and diagonal key moments.
  * Replaces `_pooled(k)`, `_pooled(v)` (kernels.py:185-190, kernel `_pool`
  * kernels.py:16-27) and `_moments` (kernels.py:30-49).
- * kc/vct receive BF16 (round-to-nearest-even) 64-token block means; when
- * key_mean/key_var/chunk_sums are all non-NULL, also the per-(batch, head,
- * feature) population mean and clamped variance of the BF16 centroids. */
+ * kc/vct receive BF16 (round-to-nearest-even) 64-token block means (both NULL:
+ * tiles only); tiles receives every key block as the swizzled K / V^T tile
+ * pair the attention kernels stream; when key_mean/key_var/chunk_sums are all
+ * non-NULL, also the per-(batch, head, feature) population mean and clamped
+ * variance of the BF16 centroids. */
 int sol_pool_kv(const void* k, const int64_t* k_strides,
                 const void* v, const int64_t* v_strides,
                 const int64_t* key_index,
                 int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
-                void* kc, void* vct, float* chunk_sums, float* key_mean, float* key_var,
+                void* kc, void* vct, void* tiles,
+                float* chunk_sums, float* key_mean, float* key_var,
                 void* stream);
 
-/* Fused routing + attention over pooled keys.
+/* Fused routing + attention over the pooled keys of sol_pool_kv.
  * Replaces the `_threshold` and `_sol` launches of `launch_sol`
  * (kernels.py:203-225; kernels kernels.py:52-64 and 101-182).
  * beta: finite, -INFINITY (every block exact) or +INFINITY (protected blocks
@@ -81,11 +85,9 @@ int sol_pool_kv(const void* k, const int64_t* k_strides,
  * routing decisions and proxies (natural-log units); debug_cutoff: NULL or
  * fp32 [batch, NQB, heads].  Debug outputs are for verification, not timing. */
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
-                      const void* k, const int64_t* k_strides,
-                      const void* v, const int64_t* v_strides, const int64_t* key_index,
                       int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       int64_t heads, int64_t head_dim,
-                      const void* kc, const void* vct,
+                      const void* tiles, const void* kc, const void* vct,
                       const float* key_mean, const float* key_var,
                       const uint8_t* protection,
                       double scale, double beta, int64_t local_blocks,
@@ -96,13 +98,14 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
 
 /* Non-causal BF16 attention over all keys, FP32 softmax and accumulation.
  * Replaces `launch_dense` (kernels.py:193-200; kernel kernels.py:67-98).
+ * tiles: workspace of sol_pool_sizes()[4] bytes (filled here).
  * out: contiguous BF16 [batch, query_tokens, heads, head_dim]. */
 int sol_dense_fwd(const void* q, const int64_t* q_strides,
                   const void* k, const int64_t* k_strides,
                   const void* v, const int64_t* v_strides,
                   int64_t batch, int64_t query_tokens, int64_t key_tokens,
                   int64_t heads, int64_t head_dim, double scale,
-                  void* out, void* stream);
+                  void* tiles, void* out, void* stream);
 
 #ifdef __cplusplus
 }

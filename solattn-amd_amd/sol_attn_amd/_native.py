@@ -33,14 +33,13 @@ _SIGNATURES = {
     "sol_last_error": ([], ctypes.c_char_p),
     "sol_pool_sizes": ([_i64, _i64, _i64, _i64, _i64p], ctypes.c_int),
     "sol_pool_kv": ([_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64,
-                     _p, _p, _p, _p, _p, _p], ctypes.c_int),
-    "sol_attention_fwd": ([_p, _i64p, _p, _p, _i64p, _p, _i64p, _p,
-                           _i64, _i64, _i64, _i64, _i64,
-                           _p, _p, _p, _p, _p,
+                     _p, _p, _p, _p, _p, _p, _p], ctypes.c_int),
+    "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _i64,
+                           _p, _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
                            _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
-                       _dbl, _p, _p], ctypes.c_int),
+                       _dbl, _p, _p, _p], ctypes.c_int),
 }
 
 
@@ -92,12 +91,17 @@ def _rows(x):
     return x if _aligned(x) else x.clone(memory_format=torch.contiguous_format)
 
 
+def _tiles(b, h, nkb, d, device):
+    return torch.empty((b, h, nkb, 2, BLOCK * d), device=device, dtype=torch.bfloat16)
+
+
 def pool_kv(k, v, key_index=None, moments=True):
-    """K/V centroids (and key moments) as the attention kernel consumes them.
+    """K/V centroids, attention tiles and key moments (one HBM pass over K and V).
 
     ``k``/``v``: ``[B, Tk, H, D]`` BF16 or, with ``key_index`` ``[B, Tk]``,
     NHD ``[N, H, D]``.  Returns a dict with ``kc`` ``[B, H, NKB, D]``,
-    ``vct`` ``[B, H, D, NKBP]``, ``mean``/``var`` ``[B, H, D]`` (or None).
+    ``vct`` ``[B, H, D, NKBP]``, ``tiles`` ``[B, H, NKB, 2, 64 D]`` and
+    ``mean``/``var`` ``[B, H, D]`` (None without ``moments``).
     """
     lib = library()
     indexed = key_index is not None
@@ -112,36 +116,34 @@ def pool_kv(k, v, key_index=None, moments=True):
     dev = k.device
     kc = torch.empty((b, h, nkb, d), device=dev, dtype=torch.bfloat16)
     vct = torch.empty((b, h, d, nkbp), device=dev, dtype=torch.bfloat16)
+    tiles = _tiles(b, h, nkb, d, dev)
     mean = var = sums = None
     if moments:
         sums = torch.empty((b, h, -(-nkb // 16), 2, d), device=dev, dtype=torch.float32)
         mean = torch.empty((b, h, d), device=dev, dtype=torch.float32)
         var = torch.empty_like(mean)
     _check(lib.sol_pool_kv(_ptr(k), _strides(k, indexed), _ptr(v), _strides(v, indexed),
-                           _ptr(key_index), b, tk, h, d, _ptr(kc), _ptr(vct), _ptr(sums),
-                           _ptr(mean), _ptr(var), _stream(dev)))
-    return {"kc": kc, "vct": vct, "mean": mean, "var": var}
+                           _ptr(key_index), b, tk, h, d, _ptr(kc), _ptr(vct), _ptr(tiles),
+                           _ptr(sums), _ptr(mean), _ptr(var), _stream(dev)))
+    return {"kc": kc, "vct": vct, "tiles": tiles, "mean": mean, "var": var, "key_tokens": tk}
 
 
-def attend(q, k, v, pooled, scale, beta, local, kv_sink, q_sink, protection=None,
-           rows=None, keys=None, debug=False):
+def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows=None,
+           debug=False):
     """Routing + attention over pooled keys (the ``_sol`` launch of ``kernels.py:218-224``).
 
-    ``pooled`` is the dict returned by :func:`pool_kv` for the same keys.
-    Returns ``(out, counts, dbg)``; ``dbg`` is None unless ``debug``.
+    ``pooled`` is the dict returned by :func:`pool_kv`.  ``rows`` (indexed
+    windows) gathers the query rows.  Returns ``(out, counts, dbg)``; ``dbg``
+    is None unless ``debug``.
     """
     lib = library()
-    indexed = keys is not None
-    if indexed:
-        b, nq = rows.shape
-        nk = keys.shape[1]
-        h, d = q.shape[-2:]
-    else:
-        b, nq, h, d = q.shape
-        nk = k.shape[1]
-    q, k, v = _rows(q), _rows(k), _rows(v)
+    indexed = rows is not None
+    b, h, nkb, d = pooled["kc"].shape
+    nq = rows.shape[1] if indexed else q.shape[1]
+    nk = pooled["key_tokens"]
+    q = _rows(q)
     dev = q.device
-    nqb, nkb = -(-nq // BLOCK), -(-nk // BLOCK)
+    nqb = -(-nq // BLOCK)
     out = torch.empty((b, nq, h, d), device=dev, dtype=torch.bfloat16)
     counts = torch.empty((b, nqb, h), device=dev, dtype=torch.int32)
     dbg = None
@@ -153,9 +155,9 @@ def attend(q, k, v, pooled, scale, beta, local, kv_sink, q_sink, protection=None
     if protection is not None:
         prot = protection.contiguous().view(torch.uint8)
     _check(lib.sol_attention_fwd(
-        _ptr(q), _strides(q, indexed), _ptr(rows), _ptr(k), _strides(k, indexed), _ptr(v),
-        _strides(v, indexed), _ptr(keys), b, nq, nk, h, d,
-        _ptr(pooled["kc"]), _ptr(pooled["vct"]), _ptr(pooled["mean"]), _ptr(pooled["var"]),
+        _ptr(q), _strides(q, indexed), _ptr(rows), b, nq, nk, h, d,
+        _ptr(pooled["tiles"]), _ptr(pooled["kc"]), _ptr(pooled["vct"]),
+        _ptr(pooled["mean"]), _ptr(pooled["var"]),
         _ptr(prot), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
         _ptr(out), _ptr(counts),
         _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
@@ -173,9 +175,9 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
     kernels instead of materialising copies.  Returns ``(out, counts)`` and,
     with ``debug=True``, a dict of routing diagnostics as a third element.
     """
-    pooled = pool_kv(_rows(k), _rows(v), key_index=keys, moments=not math.isinf(beta))
-    out, counts, dbg = attend(q, k, v, pooled, scale, beta, local, kv_sink, q_sink,
-                              protection, rows, keys, debug)
+    pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta))
+    out, counts, dbg = attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection, rows,
+                              debug)
     if debug:
         dbg.update(pooled)
         return out, counts, dbg
@@ -187,8 +189,10 @@ def launch_dense(q, k, v, scale):
     lib = library()
     q, k, v = _rows(q), _rows(k), _rows(v)
     b, nq, h, d = q.shape
+    nk = k.shape[1]
     out = torch.empty((b, nq, h, d), device=q.device, dtype=torch.bfloat16)
+    tiles = _tiles(b, h, -(-nk // BLOCK), d, q.device)
     _check(lib.sol_dense_fwd(_ptr(q), _strides(q), _ptr(k), _strides(k), _ptr(v), _strides(v),
-                             b, nq, k.shape[1], h, d, float(scale), _ptr(out),
+                             b, nq, nk, h, d, float(scale), _ptr(tiles), _ptr(out),
                              _stream(q.device)))
     return out

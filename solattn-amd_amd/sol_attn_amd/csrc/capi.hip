@@ -61,7 +61,7 @@ int sol_abi_version(void) { return SOL_ABI_VERSION; }
 const char* sol_last_error(void) { return g_last_error.c_str(); }
 
 int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
-                   int64_t sizes[4]) {
+                   int64_t sizes[5]) {
   if (!sizes || !shape_ok(batch, key_tokens, heads, head_dim))
     return fail(SOL_ERR_INVALID, "sol_pool_sizes: invalid shape");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
@@ -70,31 +70,41 @@ int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t hea
   sizes[1] = batch * heads * head_dim * nkbp * 2;
   sizes[2] = batch * heads * cdiv(nkb, 16) * 2 * head_dim * 4;
   sizes[3] = batch * heads * head_dim * 4;
+  sizes[4] = batch * heads * nkb * 2 * SOL_BLOCK * head_dim * 2;
   return SOL_OK;
 }
 
-int sol_pool_kv(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
-                const int64_t* key_index, int64_t batch, int64_t key_tokens, int64_t heads,
-                int64_t head_dim, void* kc, void* vct, float* chunk_sums, float* key_mean,
-                float* key_var, void* stream) {
+namespace {
+
+int pool_checked(const char* who, const void* k, const int64_t* k_strides, const void* v,
+                 const int64_t* v_strides, const int64_t* key_index, int64_t batch,
+                 int64_t key_tokens, int64_t heads, int64_t head_dim, void* kc, void* vct,
+                 void* tiles, float* chunk_sums, float* key_mean, float* key_var, void* stream) {
+  static thread_local std::string msg;
+  auto err = [&](int code, const char* what) {
+    msg = std::string(who) + ": " + what;
+    return fail(code, msg.c_str());
+  };
   if (!shape_ok(batch, key_tokens, heads, head_dim))
-    return fail(SOL_ERR_INVALID, "sol_pool_kv: unsupported shape (head_dim must be 64 or 128)");
+    return err(SOL_ERR_INVALID, "unsupported shape (head_dim must be 64 or 128)");
   const bool indexed = key_index != nullptr;
   if (!operand_ok(k, k_strides, indexed) || !operand_ok(v, v_strides, indexed))
-    return fail(SOL_ERR_INVALID, "sol_pool_kv: K/V need 16-byte aligned rows and positive strides");
-  if (!kc || !vct || !aligned16(kc) || !aligned16(vct))
-    return fail(SOL_ERR_INVALID, "sol_pool_kv: kc/vct must be 16-byte aligned device buffers");
+    return err(SOL_ERR_INVALID, "K/V need 16-byte aligned rows and positive strides");
+  if (bool(kc) != bool(vct)) return err(SOL_ERR_INVALID, "kc and vct go together");
+  if (!kc && !tiles) return err(SOL_ERR_INVALID, "nothing to write");
+  if ((kc && (!aligned16(kc) || !aligned16(vct))) || (tiles && !aligned16(tiles)))
+    return err(SOL_ERR_INVALID, "kc/vct/tiles must be 16-byte aligned device buffers");
   const bool moments = chunk_sums || key_mean || key_var;
-  if (moments && !(chunk_sums && key_mean && key_var))
-    return fail(SOL_ERR_INVALID, "sol_pool_kv: chunk_sums, key_mean and key_var go together");
+  if (moments && !(chunk_sums && key_mean && key_var && kc))
+    return err(SOL_ERR_INVALID, "chunk_sums, key_mean and key_var go together (with kc)");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
-  if (nkb > (int64_t(1) << 19))
-    return fail(SOL_ERR_UNSUPPORTED, "sol_pool_kv: too many key blocks");
+  if (nkb > (int64_t(1) << 19)) return err(SOL_ERR_UNSUPPORTED, "too many key blocks");
   sol::PoolParams p;
   p.k = rows_of(k, k_strides, key_index, key_tokens);
   p.v = rows_of(v, v_strides, key_index, key_tokens);
   p.kc = static_cast<uint16_t*>(kc);
   p.vct = static_cast<uint16_t*>(vct);
+  p.tiles = static_cast<uint16_t*>(tiles);
   p.ksum = moments ? chunk_sums : nullptr;
   p.mean = key_mean;
   p.var = key_var;
@@ -107,31 +117,38 @@ int sol_pool_kv(const void* k, const int64_t* k_strides, const void* v, const in
   return hip_status(sol::launch_pool(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
+}  // namespace
+
+int sol_pool_kv(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                const int64_t* key_index, int64_t batch, int64_t key_tokens, int64_t heads,
+                int64_t head_dim, void* kc, void* vct, void* tiles, float* chunk_sums,
+                float* key_mean, float* key_var, void* stream) {
+  return pool_checked("sol_pool_kv", k, k_strides, v, v_strides, key_index, batch, key_tokens,
+                      heads, head_dim, kc, vct, tiles, chunk_sums, key_mean, key_var, stream);
+}
+
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
-                      const void* k, const int64_t* k_strides, const void* v,
-                      const int64_t* v_strides, const int64_t* key_index, int64_t batch,
-                      int64_t query_tokens, int64_t key_tokens, int64_t heads, int64_t head_dim,
-                      const void* kc, const void* vct, const float* key_mean,
-                      const float* key_var, const uint8_t* protection, double scale,
-                      double beta, int64_t local_blocks, int64_t kv_sink_tokens,
+                      int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                      int64_t head_dim, const void* tiles, const void* kc, const void* vct,
+                      const float* key_mean, const float* key_var, const uint8_t* protection,
+                      double scale, double beta, int64_t local_blocks, int64_t kv_sink_tokens,
                       int64_t query_sink_tokens, void* out, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
                       void* stream) {
   if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
       key_tokens >= (int64_t(1) << 30))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: unsupported shape (head_dim must be 64 or 128)");
-  if (!operand_ok(q, q_strides, query_index != nullptr) ||
-      !operand_ok(k, k_strides, key_index != nullptr) ||
-      !operand_ok(v, v_strides, key_index != nullptr))
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: Q/K/V need 16-byte aligned rows and positive strides");
+  if (!operand_ok(q, q_strides, query_index != nullptr))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: Q needs 16-byte aligned rows and positive strides");
   if (!std::isfinite(scale) || scale <= 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: scale must be finite and positive");
   if (std::isnan(beta)) return fail(SOL_ERR_INVALID, "sol_attention_fwd: beta must not be NaN");
   if (kv_sink_tokens < 0 || query_sink_tokens < 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: sink token counts must be nonnegative");
   const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
-  if (!kc || !vct || !aligned16(kc) || !aligned16(vct) || !out || !aligned16(out))
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: kc/vct/out must be 16-byte aligned device buffers");
+  if (!tiles || !kc || !vct || !aligned16(tiles) || !aligned16(kc) || !aligned16(vct) || !out ||
+      !aligned16(out))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: tiles/kc/vct/out must be 16-byte aligned device buffers");
   if (force == 0 && (!key_mean || !key_var))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
@@ -141,9 +158,9 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   if (batch * heads * nqb >= (int64_t(1) << 31))
     return fail(SOL_ERR_UNSUPPORTED, "sol_attention_fwd: grid too large");
   sol::AttnParams p;
+  std::memset(&p, 0, sizeof(p));
   p.q = rows_of(q, q_strides, query_index, query_tokens);
-  p.k = rows_of(k, k_strides, key_index, key_tokens);
-  p.v = rows_of(v, v_strides, key_index, key_tokens);
+  p.tiles = static_cast<const uint16_t*>(tiles);
   p.kc = static_cast<const uint16_t*>(kc);
   p.vct = static_cast<const uint16_t*>(vct);
   p.mean = key_mean;
@@ -175,23 +192,25 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
 int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
                   const int64_t* k_strides, const void* v, const int64_t* v_strides,
                   int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
-                  int64_t head_dim, double scale, void* out, void* stream) {
+                  int64_t head_dim, double scale, void* tiles, void* out, void* stream) {
   if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
       key_tokens >= (int64_t(1) << 30))
     return fail(SOL_ERR_INVALID, "sol_dense_fwd: unsupported shape (head_dim must be 64 or 128)");
-  if (!operand_ok(q, q_strides, false) || !operand_ok(k, k_strides, false) ||
-      !operand_ok(v, v_strides, false))
-    return fail(SOL_ERR_INVALID, "sol_dense_fwd: Q/K/V need 16-byte aligned rows and positive strides");
+  if (!operand_ok(q, q_strides, false))
+    return fail(SOL_ERR_INVALID, "sol_dense_fwd: Q needs 16-byte aligned rows and positive strides");
   if (!std::isfinite(scale) || scale <= 0)
     return fail(SOL_ERR_INVALID, "sol_dense_fwd: scale must be finite and positive");
   if (!out || !aligned16(out)) return fail(SOL_ERR_INVALID, "sol_dense_fwd: out must be 16-byte aligned");
   if (batch * heads * cdiv(query_tokens, 128) >= (int64_t(1) << 31))
     return fail(SOL_ERR_UNSUPPORTED, "sol_dense_fwd: grid too large");
+  const int rc = pool_checked("sol_dense_fwd", k, k_strides, v, v_strides, nullptr, batch,
+                              key_tokens, heads, head_dim, nullptr, nullptr, tiles, nullptr,
+                              nullptr, nullptr, stream);
+  if (rc != SOL_OK) return rc;
   sol::AttnParams p;
   std::memset(&p, 0, sizeof(p));
   p.q = rows_of(q, q_strides, nullptr, query_tokens);
-  p.k = rows_of(k, k_strides, nullptr, key_tokens);
-  p.v = rows_of(v, v_strides, nullptr, key_tokens);
+  p.tiles = static_cast<const uint16_t*>(tiles);
   p.out = static_cast<uint16_t*>(out);
   p.B = int(batch);
   p.H = int(heads);

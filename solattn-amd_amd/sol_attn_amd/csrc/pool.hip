@@ -2,11 +2,13 @@
 //
 // Replaces the reference's `_pool` + `_pooled` (src/sol_attn_amd/kernels.py:16-27,
 // 185-190) and `_moments` (kernels.py:30-49).  HBM-bound: every K and V token
-// row is read exactly once with 16-byte loads; centroids are written in the
-// layouts the attention kernel consumes:
-//   KC  [B, H, NKB, D]   bf16, one contiguous row per key block
-//   VCt [B, H, D, NKBP]  bf16, key blocks contiguous per feature (NKBP = NKB
-//                        rounded up to 32, zero padded) -> MFMA A operand
+// row is read exactly once with 16-byte loads (through the index for indexed
+// windows); the outputs are written in the layouts the attention kernels use:
+//   KC    [B, H, NKB, D]   bf16, one contiguous row per key block
+//   VCt   [B, H, D, NKBP]  bf16, key blocks contiguous per feature (NKBP = NKB
+//                          rounded up to 32, zero padded) -> MFMA A operand
+//   tiles [B, H, NKB, 2, 64 D] swizzled K and V^T block tiles (TileLayout),
+//                          streamed by the exact-block loop with LDS DMA
 // Sums follow torch's CPU outer-reduction order (16-row sequential chunks,
 // folded in order), so the FP32 means and the BF16-rounded centroids equal the
 // reference oracle's `x[:, i:i+64].float().mean(1)` bit for bit.
@@ -24,6 +26,7 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
   constexpr int DC = D / 8;          // 16-byte chunks per token row
   constexpr int LPB = DC * 4;        // lanes per key block: 4 chunks of 16 rows
   constexpr int BPI = kWave / LPB;   // key blocks per wave iteration
+  using TL = TileLayout<D>;
   __shared__ __align__(16) uint16_t cent[kPoolChunk][D];
 
   const bool is_v = blockIdx.y != 0;
@@ -49,6 +52,31 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
       for (int i = 0; i < 16; ++i) {
         const int t = 16 * r4 + i;
         x[i] = t < len ? load16(src.row(b, kBlock * j + t, h) + 8 * dc) : zero_u32x4();
+      }
+      if (p.tiles) {
+        // Attention-ready tiles: K rows as loaded, V transposed 8x8 in registers.
+        uint16_t* tile = p.tiles + ((int64_t(b) * p.H + h) * p.NKB + j) * 2 * TL::kElems;
+        if (!is_v) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            *reinterpret_cast<u32x4*>(tile + TL::k_offset(16 * r4 + i, dc)) = x[i];
+        } else {
+          uint16_t* vt = tile + TL::kElems;
+#pragma unroll
+          for (int sb = 0; sb < 2; ++sb) {
+            u32x4 rows[8], cols[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rows[i] = x[8 * sb + i];
+            transpose8x8(rows, cols);
+            const int g0 = 4 * r4 + 2 * sb;  // 4-key group of keys 16 r4 + 8 sb
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int d = 8 * dc + e;
+              *reinterpret_cast<u32x2*>(vt + TL::vt_offset(d, g0)) = u32x2{cols[e][0], cols[e][1]};
+              *reinterpret_cast<u32x2*>(vt + TL::vt_offset(d, g0 + 1)) = u32x2{cols[e][2], cols[e][3]};
+            }
+          }
+        }
       }
       // Sequential accumulation inside the 16-row chunk (torch order).
 #pragma unroll
@@ -88,6 +116,7 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
   __syncthreads();
 
   const int64_t head = int64_t(b) * p.H + h;
+  if (!p.kc) return;  // tiles only (dense path)
   if (!is_v) {
     if (tid < kPoolChunk * DC) {
       const int jb = tid / DC, cc = tid % DC;
@@ -149,7 +178,7 @@ hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
   else
     hipLaunchKernelGGL(pool_kv_kernel<64>, grid, dim3(256), 0, stream, p);
   hipError_t err = hipGetLastError();
-  if (err != hipSuccess || !p.ksum) return err;
+  if (err != hipSuccess || !p.ksum || !p.kc) return err;
   if (D == 128)
     hipLaunchKernelGGL(moments_kernel<128>, dim3(p.B * p.H), dim3(128), 0, stream,
                        p.ksum, p.mean, p.var, p.NKB);

@@ -99,6 +99,24 @@ __device__ __forceinline__ void transpose8x8(const u32x4 (&in)[8], u32x4 (&out)[
   }
 }
 
+// Block tiles written by the pooling pass and streamed by the attention kernels.
+// Per (batch, head, key block): a K tile (64 keys x D, row-major) followed by a
+// V^T tile (D features x 64 keys).  Both are swizzled so that the MFMA operand
+// reads from LDS are bank-conflict free and a tile is one contiguous copy:
+//   K tile:   16-byte chunk c of key row r sits at chunk c ^ (r & 7)
+//   V^T tile: 8-byte group g (4 keys) of feature row d sits at group g ^ (d & 15)
+// Keys past the end of the sequence are zero in both tiles.
+template <int D>
+struct TileLayout {
+  static constexpr int kElems = kBlock * D;   // elements per K (or V^T) tile
+  __device__ static __forceinline__ int k_offset(int row, int chunk) {
+    return row * D + 8 * (chunk ^ (row & 7));
+  }
+  __device__ static __forceinline__ int vt_offset(int d, int group) {
+    return d * kBlock + 4 * (group ^ (d & 15));
+  }
+};
+
 // Torch-order fold of a block-axis reduction made of 16-row chunk sums.
 // Chunk sums arrive in order; full chunks cascade through three levels
 // (carry every 16 rows, again every 256, again every 4096); a trailing partial

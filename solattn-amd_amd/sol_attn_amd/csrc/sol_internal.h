@@ -10,16 +10,18 @@ namespace sol {
 
 struct PoolParams {
   TokenRows k, v;
-  uint16_t* kc;   // [B, H, NKB, D]
-  uint16_t* vct;  // [B, H, D, NKBP]
-  float* ksum;    // [B, H, NCH, 2, D] chunk sums, null -> no moments
-  float* mean;    // [B, H, D]
-  float* var;     // [B, H, D]
+  uint16_t* kc;     // [B, H, NKB, D] or null (no centroids)
+  uint16_t* vct;    // [B, H, D, NKBP] or null
+  uint16_t* tiles;  // [B, H, NKB, 2, 64 * D] swizzled K / V^T block tiles, or null
+  float* ksum;      // [B, H, NCH, 2, D] chunk sums, null -> no moments
+  float* mean;      // [B, H, D]
+  float* var;       // [B, H, D]
   int B, H, Tk, NKB, NKBP, NCHP;
 };
 
 struct AttnParams {
-  TokenRows q, k, v;
+  TokenRows q;
+  const uint16_t* tiles;       // [B, H, NKB, 2, 64 * D] from the pooling pass
   const uint16_t* kc;          // [B, H, NKB, D]
   const uint16_t* vct;         // [B, H, D, NKBP]
   const float* mean;           // [B, H, D]

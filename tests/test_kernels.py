@@ -28,6 +28,29 @@ def kernel_pool(k, v, moments=True):
         return _native.pool_kv(k, v, moments=moments)
 
 
+def check_tiles(tiles, k, v):
+    """Un-swizzle the attention tiles on the CPU and compare with K / V^T blocks."""
+    t = tiles.cpu().view(torch.int16).numpy().view(np.uint16)   # [B, H, NKB, 2, 64 D]
+    kb = k.contiguous().view(torch.int16).numpy().view(np.uint16)
+    vb = v.contiguous().view(torch.int16).numpy().view(np.uint16)
+    b, h, nkb, _, e = t.shape
+    d = e // 64
+    tk = kb.shape[1]
+    pad = nkb * 64 - tk
+    kp = np.concatenate([kb, np.zeros((b, pad) + kb.shape[2:], np.uint16)], 1)
+    vp = np.concatenate([vb, np.zeros((b, pad) + vb.shape[2:], np.uint16)], 1)
+    kt = t[:, :, :, 0].reshape(b, h, nkb, 64, d // 8, 8)
+    rows = np.arange(64)[:, None]
+    chunks = np.arange(d // 8)[None, :]
+    k_unswz = kt[:, :, :, rows, chunks ^ (rows & 7)].reshape(b, h, nkb, 64, d)
+    np.testing.assert_array_equal(k_unswz, kp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 2, 4))
+    vt = t[:, :, :, 1].reshape(b, h, nkb, d, 16, 4)
+    dd = np.arange(d)[:, None]
+    groups = np.arange(16)[None, :]
+    v_unswz = vt[:, :, :, dd, groups ^ (dd & 15)].reshape(b, h, nkb, d, 64)
+    np.testing.assert_array_equal(v_unswz, vp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 4, 2))
+
+
 @pytest.mark.parametrize("shape", [(1, 317, 2, 64), (2, 1089, 3, 128), (1, 1, 1, 64), (2, 4096, 16, 128),
                                    (1, 10000, 4, 128)])
 def test_pooling_and_moments_bit_exact(shape):
@@ -37,6 +60,7 @@ def test_pooling_and_moments_bit_exact(shape):
     v = torch.randn(shape, generator=g, dtype=torch.bfloat16)
     out = kernel_pool(k.cuda(), v.cuda())
     torch.cuda.synchronize()
+    check_tiles(out["tiles"], k, v)
     kc = orc.block_means(to_np(k), True)          # [B, NKB, H, D]
     vc = orc.block_means(to_np(v), True)
     mean, var = orc.key_moments(kc)
@@ -56,6 +80,7 @@ def test_pooling_strided_and_indexed_gather():
     k = base.cuda()[:, ::2]                     # NHD, head stride 128 elements
     v = (base.cuda() * 2)[:, 1::2]
     out = _native.pool_kv(k, v, key_index=keys.cuda())
+    check_tiles(out["tiles"], k.cpu()[keys], v.cpu()[keys])
     kc = orc.block_means(to_np(k.cpu()[keys]), True)
     vc = orc.block_means(to_np(v.cpu()[keys]), True)
     np.testing.assert_array_equal(to_np(out["kc"]).transpose(0, 2, 1, 3), kc)
