@@ -144,6 +144,8 @@ def main():
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="videodit-84672")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--dense-reps", type=int, default=2)
+    ap.add_argument("--copy-gib", type=float, default=0.0,
+                    help="also run a device copy of this many GiB (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -187,6 +189,14 @@ def main():
                                               debug=True)
         dense_ms = event_ms(lambda: dense_attention(q, k, v), args.dense_reps)
     torch.cuda.synchronize()
+    if args.copy_gib > 0:
+        # One elementwise kernel that reads and writes exactly copy_gib GiB each.
+        src = torch.empty(int(args.copy_gib * (1 << 30)) // 4, device=dev, dtype=torch.float32)
+        src.fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.mul(src, 2.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     deterministic = bool(torch.equal(ref_out, out))
     density = counts.float().mean().item() / dbg["selected"].shape[-1]
     exact_flops, approx_flops = routing_flops(dbg["selected"], t, t, d)

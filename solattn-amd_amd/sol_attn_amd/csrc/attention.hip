@@ -35,13 +35,27 @@ namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
-// Every XCD (workgroup ids are dealt round-robin over the 8 XCDs) receives a
-// contiguous range of tasks, so neighbouring query blocks of one head share
-// that XCD's L2.
-__device__ __forceinline__ int xcd_task(int i, int n) {
-  const int xcd = i & 7, slot = i >> 3;
-  const int per = n >> 3, rem = n & 7;
-  return xcd * per + min(xcd, rem) + slot;
+constexpr int kXcds = 8;
+
+// Workgroup ids are dealt round-robin over the 8 XCDs.  The id -> (head, query
+// tile) map keeps every XCD on the SAME head at the same time, each on its own
+// contiguous 1/8 slice of the query tiles: neighbouring tiles share that XCD's
+// L2, and the tiles of one head (43 MB at 84,672 tokens) are the whole live
+// set of the memory-side cache.  Grid = 8 * heads * slice; ids past the end of
+// a slice return -1 (idle workgroup).
+struct TileTask {
+  int bh, tile;
+};
+
+__device__ __forceinline__ TileTask xcd_task(int i, int ntiles) {
+  const int slice = (ntiles + kXcds - 1) / kXcds;
+  const int xcd = i % kXcds, k = i / kXcds;
+  const int tile = xcd * slice + k % slice;
+  return TileTask{tile < ntiles ? k / slice : -1, tile};
+}
+
+__host__ __device__ inline unsigned xcd_grid(int heads, int ntiles) {
+  return unsigned(kXcds) * unsigned(heads) * unsigned((ntiles + kXcds - 1) / kXcds);
 }
 
 template <int D>
@@ -265,9 +279,10 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   __shared__ float s_red[8];
   __shared__ uint32_t s_mask[kMaxKeyBlocks / 32];
 
-  const int task = xcd_task(blockIdx.x, gridDim.x);
-  const int qb = task % p.NQB;
-  const int bh = task / p.NQB;
+  const TileTask task = xcd_task(blockIdx.x, p.NQB);
+  if (task.bh < 0) return;
+  const int qb = task.tile;
+  const int bh = task.bh;
   const int h = bh % p.H, b = bh / p.H;
   const int64_t head = int64_t(b) * p.H + h;
   const int q0 = qb * kBlock;
@@ -478,9 +493,10 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   __shared__ __align__(16) uint16_t ring[RING];
 
   const int nq_tiles = (p.Tq + QROWS - 1) / QROWS;
-  const int task = xcd_task(blockIdx.x, gridDim.x);
-  const int qt = task % nq_tiles;
-  const int bh = task / nq_tiles;
+  const TileTask task = xcd_task(blockIdx.x, nq_tiles);
+  if (task.bh < 0) return;
+  const int qt = task.tile;
+  const int bh = task.bh;
   const int h = bh % p.H, b = bh / p.H;
   const int64_t head = int64_t(b) * p.H + h;
   const int q0 = qt * QROWS;
@@ -509,7 +525,7 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
 }
 
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
-  const unsigned grid = unsigned(p.B) * p.H * p.NQB;
+  const unsigned grid = xcd_grid(p.B * p.H, p.NQB);
   if (D == 128)
     hipLaunchKernelGGL(sol_attention_kernel<128>, dim3(grid), dim3(256), 0, stream, p);
   else
@@ -518,7 +534,7 @@ hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
 }
 
 hipError_t launch_dense(const AttnParams& p, int D, hipStream_t stream) {
-  const unsigned grid = unsigned(p.B) * p.H * unsigned((p.Tq + 127) / 128);
+  const unsigned grid = xcd_grid(p.B * p.H, (p.Tq + 127) / 128);
   if (D == 128)
     hipLaunchKernelGGL(dense_attention_kernel<128>, dim3(grid), dim3(256), 0, stream, p);
   else

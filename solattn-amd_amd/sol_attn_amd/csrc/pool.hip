@@ -149,24 +149,69 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
   }
 }
 
-// One workgroup per (batch, head): fold the chunk sums in torch's cascade order.
+// One workgroup per (batch, head): fold the 16-block chunk sums in torch's
+// cascade order.  The fold is sequential only between 256-block groups: the
+// sums of 16 consecutive chunks (what torch's level-1 accumulator holds when it
+// carries) are formed in parallel, then one thread per feature folds them.
+constexpr int kMomentThreads = 512;
+constexpr int kGroupsPerPass = 32;
+
 template <int D>
-__global__ __launch_bounds__(D) void moments_kernel(const float* __restrict__ ksum,
-                                                    float* __restrict__ mean,
-                                                    float* __restrict__ var, int nkb) {
-  const int bh = blockIdx.x, d = threadIdx.x;
+__global__ __launch_bounds__(kMomentThreads) void moments_kernel(const float* __restrict__ ksum,
+                                                                 float* __restrict__ mean,
+                                                                 float* __restrict__ var, int nkb) {
+  constexpr int G = kMomentThreads / D;  // threads per feature
+  __shared__ float gs[2][kGroupsPerPass][D];
+  const int bh = blockIdx.x, d = threadIdx.x % D, gi = threadIdx.x / D;
   const int nch = (nkb + kPoolChunk - 1) / kPoolChunk;
+  const int full_chunks = nkb / kPoolChunk;
+  const int full_groups = full_chunks / 16;
   const float* base = ksum + int64_t(bh) * nch * 2 * D;
-  CascadeFold f1, f2;
-  for (int c = 0; c < nch; ++c) {
-    const int rows = min(kPoolChunk, nkb - c * kPoolChunk);
-    f1.push(base[(2 * c) * D + d], rows);
-    f2.push(base[(2 * c + 1) * D + d], rows);
+  float a2[2] = {0.f, 0.f}, a3[2] = {0.f, 0.f};
+  int rows = 0;
+  for (int g0 = 0; g0 < full_groups; g0 += kGroupsPerPass) {
+    const int ng = min(kGroupsPerPass, full_groups - g0);
+    for (int m = gi; m < ng; m += G) {
+      const int c0 = (g0 + m) * 16;
+      float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s1 = s1 + base[(2 * (c0 + i)) * D + d];
+        s2 = s2 + base[(2 * (c0 + i) + 1) * D + d];
+      }
+      gs[0][m][d] = s1;
+      gs[1][m][d] = s2;
+    }
+    __syncthreads();
+    if (gi == 0) {
+      for (int m = 0; m < ng; ++m) {
+        rows += 256;
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          a2[w] = a2[w] + gs[w][m][d];
+          if ((rows & 0xF00) == 0) {
+            a3[w] = a3[w] + a2[w];
+            a2[w] = 0.f;
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (gi != 0) return;
+  float a1[2] = {0.f, 0.f}, rem[2] = {0.f, 0.f};
+  for (int c = full_groups * 16; c < full_chunks; ++c) {
+    a1[0] = a1[0] + base[(2 * c) * D + d];
+    a1[1] = a1[1] + base[(2 * c + 1) * D + d];
+  }
+  if (full_chunks < nch) {
+    rem[0] = base[(2 * full_chunks) * D + d];
+    rem[1] = base[(2 * full_chunks + 1) * D + d];
   }
   const float n = float(nkb);
-  const float m = __fdiv_rn(f1.total(), n);
-  const float sq = __fdiv_rn(f2.total(), n);
-  const float v = __fsub_rn(sq, __fmul_rn(m, m));
+  const float m = __fdiv_rn(((rem[0] + a1[0]) + a2[0]) + a3[0], n);
+  const float sq = __fdiv_rn(((rem[1] + a1[1]) + a2[1]) + a3[1], n);
+  const float v = sq - m * m;
   mean[int64_t(bh) * D + d] = m;
   var[int64_t(bh) * D + d] = v > 0.f ? v : 0.f;
 }
@@ -180,10 +225,10 @@ hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !p.ksum || !p.kc) return err;
   if (D == 128)
-    hipLaunchKernelGGL(moments_kernel<128>, dim3(p.B * p.H), dim3(128), 0, stream,
+    hipLaunchKernelGGL(moments_kernel<128>, dim3(p.B * p.H), dim3(kMomentThreads), 0, stream,
                        p.ksum, p.mean, p.var, p.NKB);
   else
-    hipLaunchKernelGGL(moments_kernel<64>, dim3(p.B * p.H), dim3(64), 0, stream,
+    hipLaunchKernelGGL(moments_kernel<64>, dim3(p.B * p.H), dim3(kMomentThreads), 0, stream,
                        p.ksum, p.mean, p.var, p.NKB);
   return hipGetLastError();
 }

@@ -101,47 +101,27 @@ __device__ __forceinline__ void transpose8x8(const u32x4 (&in)[8], u32x4 (&out)[
 
 // Block tiles written by the pooling pass and streamed by the attention kernels.
 // Per (batch, head, key block): a K tile (64 keys x D, row-major) followed by a
-// V^T tile (D features x 64 keys).  Both are swizzled so that the MFMA operand
-// reads from LDS are bank-conflict free and a tile is one contiguous copy:
-//   K tile:   16-byte chunk c of key row r sits at chunk c ^ (r & 7)
-//   V^T tile: 8-byte group g (4 keys) of feature row d sits at group g ^ (d & 15)
+// V^T tile (D features x 64 keys), one contiguous copy each.  Both are
+// swizzled so that the MFMA operand reads from LDS hit distinct banks whether
+// the LDS serves 128 or 256 bytes per clock (32 or 64 four-byte banks):
+//   K tile:   16-byte chunk c of key row r sits at chunk c ^ s_k(r), where
+//             s_k(r) = r & 15 for 256-byte rows (D = 128) and (r >> 1) & 7 for
+//             128-byte rows (D = 64); 16 consecutive rows (one 16-lane phase of
+//             a ds_read_b128) then cover all banks.
+//   V^T tile: 8-byte group g (4 keys) of feature row d sits at group
+//             g ^ (d & 15) ^ ((d >> 4) & 1): 16 consecutive rows use 16
+//             distinct groups, and 32 consecutive rows use distinct
+//             (row parity, group) pairs.
 // Keys past the end of the sequence are zero in both tiles.
 template <int D>
 struct TileLayout {
   static constexpr int kElems = kBlock * D;   // elements per K (or V^T) tile
   __device__ static __forceinline__ int k_offset(int row, int chunk) {
-    return row * D + 8 * (chunk ^ (row & 7));
+    const int sw = D == 128 ? (row & 15) : ((row >> 1) & 7);
+    return row * D + 8 * (chunk ^ sw);
   }
   __device__ static __forceinline__ int vt_offset(int d, int group) {
-    return d * kBlock + 4 * (group ^ (d & 15));
-  }
-};
-
-// Torch-order fold of a block-axis reduction made of 16-row chunk sums.
-// Chunk sums arrive in order; full chunks cascade through three levels
-// (carry every 16 rows, again every 256, again every 4096); a trailing partial
-// chunk is added first at the end: ((rem + a1) + a2) + a3.
-struct CascadeFold {
-  float a1 = 0.f, a2 = 0.f, a3 = 0.f, rem = 0.f;
-  int rows = 0;
-  __device__ __forceinline__ void push(float chunk_sum, int chunk_rows) {
-    if (chunk_rows == 16) {
-      rows += 16;
-      a1 = __fadd_rn(a1, chunk_sum);
-      if ((rows & 0xF0) == 0) {
-        a2 = __fadd_rn(a2, a1);
-        a1 = 0.f;
-        if ((rows & 0xF00) == 0) {
-          a3 = __fadd_rn(a3, a2);
-          a2 = 0.f;
-        }
-      }
-    } else {
-      rem = chunk_sum;
-    }
-  }
-  __device__ __forceinline__ float total() const {
-    return __fadd_rn(__fadd_rn(__fadd_rn(rem, a1), a2), a3);
+    return d * kBlock + 4 * (group ^ (d & 15) ^ ((d >> 4) & 1));
   }
 };
 

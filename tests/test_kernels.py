@@ -42,12 +42,13 @@ def check_tiles(tiles, k, v):
     kt = t[:, :, :, 0].reshape(b, h, nkb, 64, d // 8, 8)
     rows = np.arange(64)[:, None]
     chunks = np.arange(d // 8)[None, :]
-    k_unswz = kt[:, :, :, rows, chunks ^ (rows & 7)].reshape(b, h, nkb, 64, d)
+    swz = (rows & 15) if d == 128 else ((rows >> 1) & 7)
+    k_unswz = kt[:, :, :, rows, chunks ^ swz].reshape(b, h, nkb, 64, d)
     np.testing.assert_array_equal(k_unswz, kp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 2, 4))
     vt = t[:, :, :, 1].reshape(b, h, nkb, d, 16, 4)
     dd = np.arange(d)[:, None]
     groups = np.arange(16)[None, :]
-    v_unswz = vt[:, :, :, dd, groups ^ (dd & 15)].reshape(b, h, nkb, d, 64)
+    v_unswz = vt[:, :, :, dd, groups ^ (dd & 15) ^ ((dd >> 4) & 1)].reshape(b, h, nkb, d, 64)
     np.testing.assert_array_equal(v_unswz, vp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 4, 2))
 
 
