@@ -202,8 +202,7 @@ def main():
     exact_flops, approx_flops = routing_flops(dbg["selected"], t, t, d)
     attn_tflops = (exact_flops + approx_flops) / (attn_ms * 1e-3) / 1e12
     # Algorithmic pooling bytes: read K and V once; write centroids and the K / V^T tiles.
-    pool_bytes = (2 * b * t * h * d * 2 + pooled["kc"].numel() * 2 + pooled["vct"].numel() * 2
-                  + pooled["tiles"].numel() * 2)
+    pool_bytes = 2 * b * t * h * d * 2 + (pooled["ctiles"].numel() + pooled["tiles"].numel()) * 2
     pool_gbs = pool_bytes / (pool_ms * 1e-3) / 1e9
 
     result = {

@@ -46,29 +46,32 @@ int sol_abi_version(void);
 const char* sol_last_error(void);
 
 /* Byte sizes of the pooling outputs for a problem (reference: the torch.empty
- * calls of kernels.py:187,207,211-212):
- *   sizes[0] kc          bf16 [batch, heads, NKB, head_dim]
- *   sizes[1] vct         bf16 [batch, heads, head_dim, NKBP]  (NKBP = NKB rounded up to 32)
+ * calls of kernels.py:187,207,211-212), with NKB = ceil(key_tokens / 64) key
+ * blocks and NCT = ceil(NKB / 64) centroid tiles:
+ *   sizes[0] ctiles      bf16 [batch, heads, NCT, 2, 64 * head_dim]  block centroids
+ *   sizes[1] tiles       bf16 [batch, heads, NKB, 2, 64 * head_dim]  K and V^T block tiles
  *   sizes[2] chunk_sums  fp32 [batch, heads, ceil(NKB/16), 2, head_dim]
  *   sizes[3] key_mean    fp32 [batch, heads, head_dim]  (key_var has the same size)
- *   sizes[4] tiles       bf16 [batch, heads, NKB, 2, 64 * head_dim]  K and V^T block tiles
- * with NKB = ceil(key_tokens / 64). */
+ * Tile pairs: a K tile (64 rows x head_dim) then a V^T tile (head_dim rows x 64),
+ * bank-swizzled: 16-byte chunk c of K row r at chunk c ^ (r & 15) (head_dim 128)
+ * or c ^ ((r >> 1) & 7) (head_dim 64); 4-element group g of V^T row d at group
+ * g ^ (d & 15) ^ ((d >> 4) & 1).  Rows past the last key / block are zero. */
 int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
-                   int64_t sizes[5]);
+                   int64_t sizes[4]);
 
-/* K/V block pooling, attention tiles and diagonal key moments.
- * Replaces `_pooled(k)`, `_pooled(v)` (kernels.py:185-190, kernel `_pool`
- * kernels.py:16-27) and `_moments` (kernels.py:30-49).
- * kc/vct receive BF16 (round-to-nearest-even) 64-token block means (both NULL:
- * tiles only); tiles receives every key block as the swizzled K / V^T tile
- * pair the attention kernels stream; when key_mean/key_var/chunk_sums are all
+/* K/V block pooling, attention tiles and diagonal key moments, in one pass over
+ * K and V.  Replaces `_pooled(k)`, `_pooled(v)` (kernels.py:185-190, kernel
+ * `_pool` kernels.py:16-27) and `_moments` (kernels.py:30-49).
+ * ctiles receives the BF16 (round-to-nearest-even) 64-token block means of K
+ * and V (NULL: tiles only); tiles receives every key block as the tile pair the
+ * attention kernels stream; when key_mean/key_var/chunk_sums are all
  * non-NULL, also the per-(batch, head, feature) population mean and clamped
- * variance of the BF16 centroids. */
+ * variance of the BF16 key centroids. */
 int sol_pool_kv(const void* k, const int64_t* k_strides,
                 const void* v, const int64_t* v_strides,
                 const int64_t* key_index,
                 int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
-                void* kc, void* vct, void* tiles,
+                void* ctiles, void* tiles,
                 float* chunk_sums, float* key_mean, float* key_var,
                 void* stream);
 
@@ -87,7 +90,7 @@ int sol_pool_kv(const void* k, const int64_t* k_strides,
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       int64_t heads, int64_t head_dim,
-                      const void* tiles, const void* kc, const void* vct,
+                      const void* tiles, const void* ctiles,
                       const float* key_mean, const float* key_var,
                       const uint8_t* protection,
                       double scale, double beta, int64_t local_blocks,
@@ -98,7 +101,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
 
 /* Non-causal BF16 attention over all keys, FP32 softmax and accumulation.
  * Replaces `launch_dense` (kernels.py:193-200; kernel kernels.py:67-98).
- * tiles: workspace of sol_pool_sizes()[4] bytes (filled here).
+ * tiles: workspace of sol_pool_sizes()[1] bytes (filled here).
  * out: contiguous BF16 [batch, query_tokens, heads, head_dim]. */
 int sol_dense_fwd(const void* q, const int64_t* q_strides,
                   const void* k, const int64_t* k_strides,

@@ -33,9 +33,9 @@ _SIGNATURES = {
     "sol_last_error": ([], ctypes.c_char_p),
     "sol_pool_sizes": ([_i64, _i64, _i64, _i64, _i64p], ctypes.c_int),
     "sol_pool_kv": ([_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64,
-                     _p, _p, _p, _p, _p, _p, _p], ctypes.c_int),
+                     _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _i64,
-                           _p, _p, _p, _p, _p, _p,
+                           _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
                            _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
@@ -96,12 +96,12 @@ def _tiles(b, h, nkb, d, device):
 
 
 def pool_kv(k, v, key_index=None, moments=True):
-    """K/V centroids, attention tiles and key moments (one HBM pass over K and V).
+    """Centroid tiles, attention tiles and key moments (one HBM pass over K and V).
 
     ``k``/``v``: ``[B, Tk, H, D]`` BF16 or, with ``key_index`` ``[B, Tk]``,
-    NHD ``[N, H, D]``.  Returns a dict with ``kc`` ``[B, H, NKB, D]``,
-    ``vct`` ``[B, H, D, NKBP]``, ``tiles`` ``[B, H, NKB, 2, 64 D]`` and
-    ``mean``/``var`` ``[B, H, D]`` (None without ``moments``).
+    NHD ``[N, H, D]``.  Returns a dict with ``ctiles`` ``[B, H, NCT, 2, 64 D]``
+    (block centroids), ``tiles`` ``[B, H, NKB, 2, 64 D]`` and ``mean``/``var``
+    ``[B, H, D]`` (None without ``moments``); layouts per ``include/sol_attn_amd.h``.
     """
     lib = library()
     indexed = key_index is not None
@@ -112,10 +112,9 @@ def pool_kv(k, v, key_index=None, moments=True):
         b, tk, h, d = k.shape
     k, v = _rows(k), _rows(v)
     nkb = -(-tk // BLOCK)
-    nkbp = -(-nkb // 32) * 32
+    nct = -(-nkb // BLOCK)
     dev = k.device
-    kc = torch.empty((b, h, nkb, d), device=dev, dtype=torch.bfloat16)
-    vct = torch.empty((b, h, d, nkbp), device=dev, dtype=torch.bfloat16)
+    ctiles = _tiles(b, h, nct, d, dev)
     tiles = _tiles(b, h, nkb, d, dev)
     mean = var = sums = None
     if moments:
@@ -123,9 +122,10 @@ def pool_kv(k, v, key_index=None, moments=True):
         mean = torch.empty((b, h, d), device=dev, dtype=torch.float32)
         var = torch.empty_like(mean)
     _check(lib.sol_pool_kv(_ptr(k), _strides(k, indexed), _ptr(v), _strides(v, indexed),
-                           _ptr(key_index), b, tk, h, d, _ptr(kc), _ptr(vct), _ptr(tiles),
+                           _ptr(key_index), b, tk, h, d, _ptr(ctiles), _ptr(tiles),
                            _ptr(sums), _ptr(mean), _ptr(var), _stream(dev)))
-    return {"kc": kc, "vct": vct, "tiles": tiles, "mean": mean, "var": var, "key_tokens": tk}
+    return {"ctiles": ctiles, "tiles": tiles, "mean": mean, "var": var, "key_tokens": tk,
+            "key_blocks": nkb}
 
 
 def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows=None,
@@ -138,7 +138,9 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     """
     lib = library()
     indexed = rows is not None
-    b, h, nkb, d = pooled["kc"].shape
+    b, h, _, _, e = pooled["tiles"].shape
+    d = e // BLOCK
+    nkb = pooled["key_blocks"]
     nq = rows.shape[1] if indexed else q.shape[1]
     nk = pooled["key_tokens"]
     q = _rows(q)
@@ -156,7 +158,7 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
         prot = protection.contiguous().view(torch.uint8)
     _check(lib.sol_attention_fwd(
         _ptr(q), _strides(q, indexed), _ptr(rows), b, nq, nk, h, d,
-        _ptr(pooled["tiles"]), _ptr(pooled["kc"]), _ptr(pooled["vct"]),
+        _ptr(pooled["tiles"]), _ptr(pooled["ctiles"]),
         _ptr(pooled["mean"]), _ptr(pooled["var"]),
         _ptr(prot), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
         _ptr(out), _ptr(counts),

@@ -3,27 +3,29 @@
 // Replaces the reference's `_threshold` (src/sol_attn_amd/kernels.py:52-64),
 // `_sol` (kernels.py:101-182) and `_dense` (kernels.py:67-98).
 //
-// SOL workgroup = one 64-query block of one (batch, head), 4 waves.  Wave w
-// owns queries 32*(w&1) .. +31 and key half (w>>1) of every 64-key block, with
-// its own FP32 online-softmax state; the two key halves are merged at the end.
-//   1. Q tile -> LDS -> register fragments (MFMA B operand of S^T = K Q^T)
+// SOL workgroup = G adjacent 64-query blocks of one (batch, head), two waves
+// per query block.  Wave w owns query block w >> 1 and its queries
+// 32*(w&1) .. +31, over all 64 keys of every tile, with its own FP32
+// online-softmax state.
+//   1. Q tiles -> LDS -> register fragments (MFMA B operand of S^T = K Q^T)
 //   2. FP32 query mean (torch cascade order) and the Eq.15 cutoff
 //      c = Qc.mu + beta * sqrt(sum Qc^2 var)                    (kernels.py:58-63)
-//   3. routing: proxy_j = Qc . Kc_j (= mean over the block's rows of q_r . Kc_j),
-//      selected = proxy > c, OR sink / local / plan protection; decisions live
-//      in an LDS bitmask, never in HBM                          (kernels.py:129-143)
-//   4. centroid correction for unselected blocks, 32 centroids per MFMA tile
-//      (tiles alternate between the key-half waves):
-//      w = exp2(s - m) * valid_len, O^T += Vc^T bf16(w)^T        (kernels.py:145-158)
-//   5. exact blocks in ascending order: the pooling pass's swizzled K / V^T
-//      tiles stream into a double-buffered LDS ring with global_load_lds DMA
-//      (block i+1 lands while block i is on the matrix cores);
-//      S^T = K Q^T, online softmax, O^T += V^T bf16(P)^T           (kernels.py:159-178)
-//   6. merge the key halves, O = acc / den, BF16 store, exact count (kernels.py:179-182)
+//   3. centroid pass: the NCT centroid tiles (64 BF16 block centroids each)
+//      stream through an R-slot LDS ring fed by global_load_lds DMA.  From
+//      each tile in LDS: routing proxy_j = Qc . Kc_j (= mean over the block's
+//      rows of q_r . Kc_j), selected = proxy > c OR sink / local / plan
+//      protection, into an LDS bitmask (kernels.py:129-143); then the
+//      unselected blocks contribute w = exp2(s - m) * valid_len,
+//      O^T += Vc^T bf16(w)^T                                    (kernels.py:145-158)
+//   4. exact pass: the union over the group of the selected exact tiles
+//      (64 tokens each), ascending, through the same ring; each wave consumes
+//      the tiles its query block selected: S^T = K Q^T, online softmax,
+//      O^T += V^T bf16(P)^T                                     (kernels.py:159-178)
+//   5. O = acc / den, BF16 store, exact count                   (kernels.py:179-182)
 // Every contribution shares the FP32 online-softmax state of its wave, in log2
 // units; empty states use max 0 for the rescale (kernels.py:148-150).
-// The dense control runs step 5 over every key block, 128 queries per
-// workgroup (4 waves x 32 queries, full 64-key blocks per wave).
+// The dense control streams every exact tile, 128 queries per workgroup
+// (4 waves x 32 queries, full 64-key tiles per wave).
 #include "sol_device.h"
 #include "sol_internal.h"
 
@@ -64,7 +66,7 @@ struct Shape {
   static constexpr int DC = D / 8;   // 16-byte chunks per row
   static constexpr int KT = D / 16;  // MFMA k-steps over the head dimension
   static constexpr int DT = D / 32;  // 32-row output tiles over the head dimension
-  static constexpr int TILE = 2 * kBlock * D;  // K + V^T tile elements per key block
+  static constexpr int TILE = 2 * kBlock * D;  // K + V^T tile elements per 64-wide tile
 };
 
 // One wave's FP32 online-softmax state for its 32 queries (one per lane pair).
@@ -83,16 +85,34 @@ __device__ __forceinline__ void state_init(State<D>& st) {
   st.den = 0.f;
 }
 
-// Online-softmax update with the scores s[0..NS) (log2 units, -inf = absent).
-// Returns the probabilities in s.
-template <int D, int NS>
-__device__ __forceinline__ void softmax_update(State<D>& st, f32x16 (&s)[NS]) {
+// Max / sum of a value over the lane pair (l, l ^ 32) that shares one query.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
+// Online-softmax update with raw scores s[0..NS) (-inf = absent).  Scores are
+// scaled to log2 units inside the exponent: p = exp2(s * c - m), m the running
+// max in log2 units.  Each p is multiplied by weight(t, e) (centroid tiles:
+// the block's valid length).  Returns the probabilities in s.  The
+// accumulator rescale is skipped when no query of the wave raised its max.
+struct UnitWeight {
+  __device__ __forceinline__ float operator()(int, int) const { return 1.f; }
+};
+
+template <int D, int NS, typename Weight>
+__device__ __forceinline__ void softmax_update(State<D>& st, f32x16 (&s)[NS], float c, Weight weight) {
   float mx = kNegInf;
 #pragma unroll
   for (int t = 0; t < NS; ++t)
 #pragma unroll
     for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  mx = pair_max(mx) * c;
   const float mnew = fmaxf(st.m, mx);
   const float safe = mnew == kNegInf ? 0.f : mnew;
   const float alpha = fast_exp2(st.m - safe);
@@ -101,14 +121,16 @@ __device__ __forceinline__ void softmax_update(State<D>& st, f32x16 (&s)[NS]) {
   for (int t = 0; t < NS; ++t)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float pe = fast_exp2(s[t][e] - safe);
+      const float pe = fast_exp2(fmaf(s[t][e], c, -safe)) * weight(t, e);
       s[t][e] = pe;
       lsum += pe;
     }
   st.den = st.den * alpha + lsum;
   st.m = mnew;
+  if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-  for (int dt = 0; dt < Shape<D>::DT; ++dt) st.acc[dt] *= alpha;
+    for (int dt = 0; dt < Shape<D>::DT; ++dt) st.acc[dt] *= alpha;
+  }
 }
 
 __device__ __forceinline__ bf16x8 pack8(const f32x16& s, int base) {
@@ -120,12 +142,21 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& s, int base) {
 
 // 16-byte global -> LDS DMA per lane: lane l's bytes land at lds_base + 16 l.
 // Issued as inline assembly so that the compiler does not drain the vector
-// memory counter before every LDS read (it cannot tell the ring's two buffers
+// memory counter before every LDS read (it cannot tell the ring's buffers
 // apart); completion is awaited explicitly with wait_vmcnt before the barrier.
+// M0 (the LDS base register of the DMA) is saved and restored around it.
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
   const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);  // wave-uniform by construction
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :: "s"(base), "v"(src) : "memory", "m0");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(base), "v"(src)
+      : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_address(const void* p) {
@@ -155,58 +186,126 @@ __device__ __forceinline__ void wait_vmcnt() {
 // is not drained here.  The "memory" clobber keeps LDS accesses on their side.
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// Exact 64-key block from an LDS tile pair: key halves [kh0, kh0 + NH).
+// Returns x through an empty asm statement.  Applied to a lane index inside a
+// tile loop, it makes the addresses derived from it be formed per tile rather
+// than hoisted out of the loop, where dozens of lane-dependent offsets would
+// stay live (and spill) for the whole stream.
+__device__ __forceinline__ int fresh(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Scores of key halves [kh0, kh0 + NH) of an LDS tile pair against this
+// wave's 32 queries, plus the V^T fragments for the P V^T product.  The K
+// fragments are read and multiplied first; the V^T fragments are read after
+// the last score MFMA has issued (a scheduling barrier keeps them there), so
+// they reuse the K fragments' registers and arrive during the softmax.
 template <int D, int NH>
-__device__ __forceinline__ void exact_block(const uint16_t* buf, int j, int tk, float scale_log2,
-                                            int kh0, const bf16x8 (&qf)[Shape<D>::KT], int col,
-                                            int hh, State<D>& st) {
+__device__ __forceinline__ void tile_scores(const uint16_t* buf, int kh0,
+                                            const bf16x8 (&qf)[Shape<D>::KT], int col, int hh,
+                                            f32x16 (&p)[NH], u32x4 (&va)[NH][2][Shape<D>::DT]) {
   using S = Shape<D>;
   using TL = TileLayout<D>;
   const uint16_t* kt_lds = buf;
   const uint16_t* vt_lds = buf + TL::kElems;
-  f32x16 s[NH];
+  col = fresh(col);
+  hh = fresh(hh);
+  u32x4 ka[NH][S::KT];
 #pragma unroll
-  for (int t = 0; t < NH; ++t) {
-    s[t] = zero16();
-    const int row = 32 * (kh0 + t) + col;
+  for (int ks = 0; ks < S::KT; ++ks)
 #pragma unroll
-    for (int ks = 0; ks < S::KT; ++ks) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(kt_lds + TL::k_offset(row, 2 * ks + hh));
-      s[t] = mfma32x32x16(as_bf16x8(a), qf[ks], s[t]);
-    }
-  }
-  const bool tail = (j + 1) * kBlock > tk;
+    for (int t = 0; t < NH; ++t)
+      ka[t][ks] = *reinterpret_cast<const u32x4*>(kt_lds + TL::k_offset(32 * (kh0 + t) + col, 2 * ks + hh));
 #pragma unroll
-  for (int t = 0; t < NH; ++t)
+  for (int t = 0; t < NH; ++t) p[t] = zero16();
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      float v = s[t][e] * scale_log2;
-      if (tail && j * kBlock + 32 * (kh0 + t) + 8 * (e >> 2) + 4 * hh + (e & 3) >= tk) v = kNegInf;
-      s[t][e] = v;
-    }
-  softmax_update<D, NH>(st, s);
+  for (int ks = 0; ks < S::KT; ++ks)
+#pragma unroll
+    for (int t = 0; t < NH; ++t) p[t] = mfma32x32x16(as_bf16x8(ka[t][ks]), qf[ks], p[t]);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = 0; t < NH; ++t)
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const bf16x8 b = pack8(s[t], 8 * c);
       const int g = 8 * (kh0 + t) + 4 * c + hh;  // 4-key group of keys 32(kh0+t) + 16c + 4hh
 #pragma unroll
       for (int dt = 0; dt < S::DT; ++dt) {
         const int d = dt * 32 + col;
         const u32x2 lo = *reinterpret_cast<const u32x2*>(vt_lds + TL::vt_offset(d, g));
         const u32x2 hi = *reinterpret_cast<const u32x2*>(vt_lds + TL::vt_offset(d, g + 2));
-        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-        st.acc[dt] = mfma32x32x16(as_bf16x8(a), b, st.acc[dt]);
+        va[t][c][dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
     }
+}
+
+// O^T += V^T * bf16(P)^T for key halves [kh0, kh0 + NH).
+template <int D, int NH>
+__device__ __forceinline__ void tile_pv(const f32x16 (&p)[NH], const u32x4 (&va)[NH][2][Shape<D>::DT],
+                                        State<D>& st) {
+#pragma unroll
+  for (int t = 0; t < NH; ++t)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const bf16x8 b = pack8(p[t], 8 * c);
+#pragma unroll
+      for (int dt = 0; dt < Shape<D>::DT; ++dt)
+        st.acc[dt] = mfma32x32x16(as_bf16x8(va[t][c][dt]), b, st.acc[dt]);
+    }
+}
+
+// Key row (inside a 64-row tile) of element e of this lane's 32-key half t.
+__device__ __forceinline__ int tile_row(int t, int e, int hh) {
+  return 32 * t + 8 * (e >> 2) + 4 * hh + (e & 3);
+}
+
+// Exact 64-key block j from an LDS tile pair (both key halves).
+template <int D>
+__device__ __forceinline__ void exact_block(const uint16_t* buf, int j, int tk, float scale_log2,
+                                            const bf16x8 (&qf)[Shape<D>::KT], int col, int hh,
+                                            State<D>& st) {
+  f32x16 p[2];
+  u32x4 va[2][2][Shape<D>::DT];
+  tile_scores<D, 2>(buf, 0, qf, col, hh, p, va);
+  if ((j + 1) * kBlock > tk) {  // tail block: keys past the end are absent
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (j * kBlock + tile_row(t, e, hh) >= tk) p[t][e] = kNegInf;
+  }
+  softmax_update<D, 2>(st, p, scale_log2, UnitWeight{});
+  tile_pv<D, 2>(p, va, st);
+}
+
+// Centroid tile ct: the block centroids 64 ct + r whose bit r is set in
+// `approx` contribute logit q . Kc_j + ln(len_j) and value Vc_j; the length
+// enters as a weight on exp2(s - m).
+template <int D>
+__device__ __forceinline__ void centroid_block(const uint16_t* buf, int ct, uint64_t approx, int tk,
+                                               float scale_log2, const bf16x8 (&qf)[Shape<D>::KT],
+                                               int col, int hh, State<D>& st) {
+  f32x16 p[2];
+  u32x4 va[2][2][Shape<D>::DT];
+  tile_scores<D, 2>(buf, 0, qf, col, hh, p, va);
+  // Row of element e of half t = 4 hh + (a compile-time constant): only the
+  // lane's share is formed at run time, so nothing per element stays live.
+  const uint64_t lane_approx = approx >> (4 * hh);
+  const int lane_tokens = tk - kBlock * (kBlock * ct + 4 * hh);  // keys from the lane's first block on
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      if (!((lane_approx >> tile_row(t, e, 0)) & 1u)) p[t][e] = kNegInf;
+  auto len = [&](int t, int e) { return float(min(kBlock, lane_tokens - kBlock * tile_row(t, e, 0))); };
+  softmax_update<D, 2>(st, p, scale_log2, len);
+  tile_pv<D, 2>(p, va, st);
 }
 
 template <int D>
 __device__ __forceinline__ void store_output(const AttnParams& p, int b, int h, int t, int hh,
                                              const State<D>& st) {
   using S = Shape<D>;
-  const float den = st.den + __shfl_xor(st.den, 32);
+  const float den = pair_sum(st.den);
   if (t >= p.Tq) return;
   uint16_t* orow = p.out + ((int64_t(b) * p.Tq + t) * p.H + h) * D;
 #pragma unroll
@@ -220,45 +319,102 @@ __device__ __forceinline__ void store_output(const AttnParams& p, int b, int h, 
     }
 }
 
-// Stream a sequence of exact blocks through the double-buffered LDS ring.
-// `next()` yields block ids in order and is evaluated identically by every
-// thread (uniform control flow around the barriers).
-template <int D, int NT, int NH, typename Next>
-__device__ __forceinline__ void exact_stream(const uint16_t* head_tiles, uint16_t* ring, int count,
-                                             Next next, int tk, float scale_log2, int kh0,
-                                             const bf16x8 (&qf)[Shape<D>::KT], int wave, int lane,
-                                             State<D>& st) {
-  using S = Shape<D>;
-  constexpr int kRounds = S::TILE / 8 / NT;
-  if (count <= 0) return;
-  const int col = lane & 31, hh = lane >> 5;
-  int cur = next();
-  tile_dma<D, NT>(head_tiles + int64_t(cur) * S::TILE, ring, wave, lane);
-  for (int i = 0; i < count; ++i) {
-    const int nxt = i + 1 < count ? next() : -1;
-    if (nxt >= 0) {
-      tile_dma<D, NT>(head_tiles + int64_t(nxt) * S::TILE, ring + ((i + 1) & 1) * S::TILE, wave, lane);
-      wait_vmcnt<kRounds>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    ring_barrier();
-    exact_block<D, NH>(ring + (i & 1) * S::TILE, cur, tk, scale_log2, kh0, qf, col, hh, st);
-    ring_barrier();
-    cur = nxt;
+// Waits until at most `ahead` tiles' DMA (newest first) are still in flight.
+template <int R, int kRounds>
+__device__ __forceinline__ void wait_ahead(int ahead) {
+  static_assert(R >= 2 && R <= 4, "ring depth 2..4");
+  if (R > 3 && ahead >= 2) {
+    wait_vmcnt<2 * kRounds>();
+  } else if (R > 2 && ahead >= 1) {
+    wait_vmcnt<kRounds>();
+  } else {
+    wait_vmcnt<0>();
   }
 }
 
-// Iterates the set bits of an LDS bitmask in ascending order.
-struct MaskCursor {
-  const uint32_t* mask;
-  int word;
-  uint32_t bits;
+// Streams `count` tiles through an R-slot LDS ring: while tile i is on the
+// matrix cores, the DMA of tiles i+1 .. i+R-1 is in flight.  One barrier per
+// tile: after it, tile i is visible to every wave and every wave has finished
+// tile i-1, whose slot then receives tile i+R-1.  `next()` yields tile ids in
+// order and is evaluated identically by every thread; source(id) is the
+// tile's HBM address; process(buf, id) consumes it.  Two streams over the
+// same ring are separated by a barrier.
+template <int D, int NT, int R, typename Next, typename Source, typename Process>
+__device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next, Source source,
+                                            Process process, int wave, int lane) {
+  using S = Shape<D>;
+  constexpr int kRounds = S::TILE / 8 / NT;
+  static_assert((R & (R - 1)) == 0, "ring depth must be a power of two");
+  if (count <= 0) return;
+  int ids[R - 1];  // tiles i .. i+R-2 (uniform); shifted each iteration
+#pragma unroll
+  for (int s = 0; s < R - 1; ++s) {
+    ids[s] = s < count ? next() : 0;
+    if (s < count) tile_dma<D, NT>(source(ids[s]), ring + s * S::TILE, wave, lane);
+  }
+  for (int i = 0; i < count; ++i) {
+    wait_ahead<R, kRounds>(min(R - 2, count - 1 - i));
+    ring_barrier();
+    const int id = ids[0];
+#pragma unroll
+    for (int s = 0; s < R - 2; ++s) ids[s] = ids[s + 1];
+    if (i + R - 1 < count) {
+      const int idn = next();
+      ids[R - 2] = idn;
+      tile_dma<D, NT>(source(idn), ring + ((i + R - 1) & (R - 1)) * S::TILE, wave, lane);
+    }
+    process(ring + (i & (R - 1)) * S::TILE, id);
+  }
+}
+
+// Barrier that publishes this workgroup's LDS writes (no global-memory fence,
+// so the ring's DMA in flight is not drained).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Approximated blocks of centroid tile ct for one query block: valid blocks
+// whose routing bit is clear.
+__device__ __forceinline__ uint64_t tile_approx(const uint32_t* mask, int ct, int nkb) {
+  const int nvalid = min(64, nkb - 64 * ct);
+  const uint64_t valid = nvalid == 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+  const uint64_t sel = uint64_t(mask[2 * ct]) | (uint64_t(mask[2 * ct + 1]) << 32);
+  return valid & ~sel;
+}
+
+// Exact tiles of a SOL workgroup: the union of its G query blocks' selected
+// blocks, ascending.  The exact phase starts (word 0 loaded) on the first
+// call; the word scan never passes the last mask word and every id is below
+// nkb, so the cursor yields valid tiles even if called more than count() times.
+template <int G>
+struct UnionCursor {
+  const uint32_t* mask;  // [G][stride] routing bitmasks
+  int stride, nkb;
+  int word = -1;
+  uint32_t bits = 0u;
+
+  __device__ __forceinline__ uint32_t union_word(int w) const {
+    uint32_t u = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) u |= mask[g * stride + w];
+    return u;
+  }
+  __device__ __forceinline__ int count() const {
+    int n = 0;
+    for (int w = 0; w < (nkb + 31) / 32; ++w) n += __builtin_popcount(union_word(w));
+    return n;
+  }
   __device__ __forceinline__ int operator()() {
-    while (bits == 0) bits = mask[++word];
+    const int last = (nkb + 31) / 32 - 1;
+    if (word < 0) {
+      word = 0;
+      bits = union_word(0);
+    }
+    while (bits == 0 && word < last) bits = union_word(++word);
+    if (bits == 0) return 0;  // unreachable when called count() times
     const int j = word * 32 + __builtin_ctz(bits);
     bits &= bits - 1u;
-    return j;
+    return j < nkb ? j : 0;
   }
 };
 
@@ -269,63 +425,77 @@ struct RangeCursor {
 
 }  // namespace
 
-// __launch_bounds__(256, 2): at least two waves per SIMD (<= 256 registers).
-template <int D>
-__global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
-  using S = Shape<D>;
-  constexpr int NT = 256;
-  __shared__ __align__(16) uint16_t ring[2 * S::TILE];  // Q staging / tile ring / merge scratch
-  __shared__ float s_qm[D];
-  __shared__ float s_red[8];
-  __shared__ uint32_t s_mask[kMaxKeyBlocks / 32];
 
-  const TileTask task = xcd_task(blockIdx.x, p.NQB);
+// __launch_bounds__ second argument: minimum waves per SIMD.  Two waves per
+// SIMD leave each wave 256 VGPRs: the exact path keeps the 64-register
+// accumulator, 32 registers of Q fragments and 64 of K or V fragments live.
+template <int D, int G, int R>
+__global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p) {
+  using S = Shape<D>;
+  using TL = TileLayout<D>;
+  constexpr int NT = 128 * G;
+  constexpr int kMaskWords = kMaxKeyBlocks / 32;
+  static_assert(R * S::TILE >= G * kBlock * S::KS, "Q staging must fit in the ring");
+  __shared__ __align__(16) uint16_t ring[R * S::TILE];  // Q staging, then the tile ring
+  __shared__ float s_qm[G][D];
+  __shared__ float s_red[G][4];
+  __shared__ float s_cut[G];
+  __shared__ uint32_t s_mask[G][kMaskWords];
+
+  const TileTask task = xcd_task(blockIdx.x, (p.NQB + G - 1) / G);
   if (task.bh < 0) return;
-  const int qb = task.tile;
   const int bh = task.bh;
   const int h = bh % p.H, b = bh / p.H;
   const int64_t head = int64_t(b) * p.H + h;
-  const int q0 = qb * kBlock;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, hh = lane >> 5;
-  const int qh = wave & 1, kh = wave >> 1;
+  const int qg = wave >> 1, qh = wave & 1;  // query block in the group, query half
+  const int lt = tid & 127;                  // thread index inside the query block's 2 waves
+  const int qb0 = task.tile * G;
+  const int qb = qb0 + qg;
+  const bool live = qb < p.NQB;
+  const int nkb = p.NKB, tk = p.Tk;
+  const float scale_log2 = p.scale_log2;
 
-  // 1. Q tile -> LDS -> fragments.
-  for (int idx = tid; idx < kBlock * S::DC; idx += NT) {
+  // 1. Q tiles -> LDS -> fragments.
+  for (int idx = tid; idx < G * kBlock * S::DC; idx += NT) {
     const int r = idx / S::DC, c = idx % S::DC;
-    const int t = q0 + r;
+    const int t = qb0 * kBlock + r;
     const u32x4 x = t < p.Tq ? load16(p.q.row(b, t, h) + 8 * c) : zero_u32x4();
     *reinterpret_cast<u32x4*>(ring + r * S::KS + 8 * c) = x;
   }
   __syncthreads();
   bf16x8 qf[S::KT];
-  const int myq = 32 * qh + col;
+  const int myq = 32 * qh + col;  // query inside the block
+  {
+    const uint16_t* qrow = ring + (qg * kBlock + myq) * S::KS;
 #pragma unroll
-  for (int ks = 0; ks < S::KT; ++ks)
-    qf[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(ring + myq * S::KS + ks * 16 + 8 * hh));
+    for (int ks = 0; ks < S::KT; ++ks)
+      qf[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qrow + ks * 16 + 8 * hh));
+  }
 
-  // 2. Query mean and cutoff.
-  float cut = 0.f;
+  // 2. Query mean and cutoff per query block (sums in torch's cascade order).
   if (p.force == 0) {
-    const int qlen = min(kBlock, p.Tq - q0);
-    if (tid < D) {
+    const int qlen = live ? min(kBlock, p.Tq - qb * kBlock) : 1;
+    if (lt < D) {
       float tot = 0.f;
       for (int c = 0; c < 4; ++c) {
-        float s = 0.f;
+        float sum = 0.f;
         for (int i = 0; i < 16; ++i) {
           const int r = 16 * c + i;
-          if (r < qlen) s = __fadd_rn(s, bf16_bits_to_f32(ring[r * S::KS + tid]));
+          if (r < qlen) sum = __fadd_rn(sum, bf16_bits_to_f32(ring[(qg * kBlock + r) * S::KS + lt]));
         }
-        tot = __fadd_rn(tot, s);
+        tot = __fadd_rn(tot, sum);
       }
-      s_qm[tid] = __fdiv_rn(tot, float(qlen));
+      s_qm[qg][lt] = __fdiv_rn(tot, float(qlen));
     }
     __syncthreads();
     float a = 0.f, g = 0.f;
-    if (tid < D) {
-      const float qm = s_qm[tid];
-      a = qm * p.mean[head * D + tid];
-      g = qm * qm * p.var[head * D + tid];
+    if (lt < D) {
+      const float qm = s_qm[qg][lt];
+      a = qm * p.mean[head * D + lt];
+      g = qm * qm * p.var[head * D + lt];
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -333,154 +503,98 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
       g += __shfl_xor(g, off);
     }
     if (lane == 0) {
-      s_red[wave] = a;
-      s_red[4 + wave] = g;
+      s_red[qg][qh] = a;
+      s_red[qg][2 + qh] = g;
     }
     __syncthreads();
-    const float mu = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-    const float sg = (s_red[4] + s_red[5]) + (s_red[6] + s_red[7]);
-    cut = mu + p.beta * sqrtf(sg);
+    if (tid < G) s_cut[tid] = (s_red[tid][0] + s_red[tid][1]) + p.beta * sqrtf(s_red[tid][2] + s_red[tid][3]);
   }
-  if (p.dbg_cutoff && tid == 0)
+  __syncthreads();  // cutoffs published; Q staging is dead and the ring is free
+  const int64_t dbg_row = ((int64_t(b) * p.NQB + qb) * p.H + h) * nkb;
+  if (live && p.dbg_cutoff && lt == 0)
     p.dbg_cutoff[(int64_t(b) * p.NQB + qb) * p.H + h] =
-        p.force == 0 ? cut * p.scale : (p.force == 1 ? kNegInf : -kNegInf);
-
-  // 3. Routing decisions -> LDS bitmask.
-  const int64_t dbg_row = ((int64_t(b) * p.NQB + qb) * p.H + h) * p.NKB;
-  for (int j0 = 0; j0 < p.NKB; j0 += NT) {
-    const int j = j0 + tid;
-    bool sel = false;
-    if (j < p.NKB) {
-      if (p.force == 1) {
-        sel = true;
-      } else if (p.force == 0) {
-        const uint16_t* kr = p.kc + (head * p.NKB + j) * D;
-        float proxy = 0.f;
-#pragma unroll
-        for (int c = 0; c < S::DC; ++c) {
-          const u32x4 x = load16(kr + 8 * c);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const uint32_t w = x[e >> 1];
-            proxy = fmaf(s_qm[8 * c + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)), proxy);
-          }
-        }
-        sel = proxy > cut;
-        if (p.dbg_proxy) p.dbg_proxy[dbg_row + j] = proxy * p.scale;
-      }
-      sel = sel || (p.local_blocks >= 0 && abs(j - qb) <= p.local_blocks) ||
-            j < p.kv_sink_blocks || qb < p.q_sink_blocks;
-      if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * p.NKB + j] != 0;
-      if (p.dbg_selected) p.dbg_selected[dbg_row + j] = sel ? 1 : 0;
-    }
-    const uint64_t bal = __ballot(sel);
-    if (lane == 0) {
-      s_mask[(j0 + wave * 64) / 32] = uint32_t(bal);
-      s_mask[(j0 + wave * 64) / 32 + 1] = uint32_t(bal >> 32);
-    }
-  }
-  __syncthreads();
-  const int nwords = (p.NKB + 31) / 32;
-  int nsel = 0;
-  for (int w = 0; w < nwords; ++w) nsel += __builtin_popcount(s_mask[w]);
-  if (p.counts && tid == 0) p.counts[(int64_t(b) * p.NQB + qb) * p.H + h] = nsel;
+        p.force == 0 ? s_cut[qg] * p.scale : (p.force == 1 ? kNegInf : -kNegInf);
 
   State<D> st;
   state_init(st);
-
-  // 4. Centroid correction, 32-centroid tiles split between the key halves.
-  if (p.force != 1) {
-    const uint16_t* kc = p.kc + head * p.NKB * D;
-    const uint16_t* vct = p.vct + head * D * p.NKBP;
-    for (int t0 = 32 * kh; t0 < p.NKB; t0 += 64) {
-      const int nvalid = min(32, p.NKB - t0);
-      const uint32_t validw = nvalid == 32 ? 0xFFFFFFFFu : ((1u << nvalid) - 1u);
-      const uint32_t apw = validw & ~s_mask[t0 >> 5];
-      if (apw == 0) continue;  // wave-uniform
-      f32x16 sc[1];
-      sc[0] = zero16();
-      const bool row_ok = t0 + col < p.NKB;
+  if (p.force == 1) {
+    // 3'. beta = -inf: every block exact, no centroid pass.
+    const int nwords = (nkb + 31) / 32;
+    for (int i = tid; i < G * nwords; i += NT) {
+      const int g = i / nwords, w = i % nwords;
+      const int nvalid = min(32, nkb - 32 * w);
+      s_mask[g][w] = qb0 + g < p.NQB ? (nvalid == 32 ? ~0u : ((1u << nvalid) - 1u)) : 0u;
+    }
+    if (live && p.dbg_selected)
+      for (int j = lt; j < nkb; j += 128) p.dbg_selected[dbg_row + j] = 1;
+    __syncthreads();
+  } else {
+    // 3. Centroid pass: routing of each tile's 64 blocks (wave g routes query
+    // block qb0 + g), then the approximated blocks' contributions.
+    const uint16_t* ctiles = p.ctiles + head * p.NCT * S::TILE;
+    auto process = [&](const uint16_t* buf, int ct) {
+      if (wave < G) {
+        const int qbg = qb0 + wave;
+        const int j = kBlock * ct + lane;
+        bool sel = false;
+        if (qbg < p.NQB && j < nkb) {
+          const int64_t row = ((int64_t(b) * p.NQB + qbg) * p.H + h) * nkb;
+          if (p.force == 0) {
+            const int row_lane = fresh(lane);
+            float proxy = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < S::KT; ++ks) {
-        const u32x4 a = row_ok ? load16(kc + int64_t(t0 + col) * D + ks * 16 + 8 * hh) : zero_u32x4();
-        sc[0] = mfma32x32x16(as_bf16x8(a), qf[ks], sc[0]);
-      }
-      float mx = kNegInf;
+            for (int c = 0; c < S::DC; ++c) {
+              const u32x4 x = *reinterpret_cast<const u32x4*>(buf + TL::k_offset(row_lane, c));
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = 8 * (e >> 2) + 4 * hh + (e & 3);
-        sc[0][e] = ((apw >> r) & 1u) ? sc[0][e] * p.scale_log2 : kNegInf;
-        mx = fmaxf(mx, sc[0][e]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(st.m, mx);
-      const float safe = mnew == kNegInf ? 0.f : mnew;
-      const float alpha = fast_exp2(st.m - safe);
-      float wsum = 0.f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = 8 * (e >> 2) + 4 * hh + (e & 3);
-        // weight = exp2(s - m) * valid length; 0 for selected / padding blocks
-        const float w = ((apw >> r) & 1u)
-                            ? fast_exp2(sc[0][e] - safe) * float(min(kBlock, p.Tk - kBlock * (t0 + r)))
-                            : 0.f;
-        sc[0][e] = w;
-        wsum += w;
-      }
-      st.den = st.den * alpha + wsum;
-      st.m = mnew;
-#pragma unroll
-      for (int dt = 0; dt < S::DT; ++dt) st.acc[dt] *= alpha;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const bf16x8 bw = pack8(sc[0], 8 * c);
-#pragma unroll
-        for (int dt = 0; dt < S::DT; ++dt) {
-          const uint16_t* row = vct + int64_t(dt * 32 + col) * p.NKBP + t0 + 16 * c + 4 * hh;
-          const u32x2 lo = load8(row);
-          const u32x2 hi = load8(row + 8);
-          const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-          st.acc[dt] = mfma32x32x16(as_bf16x8(a), bw, st.acc[dt]);
+              for (int e = 0; e < 8; ++e) {
+                const uint32_t w = x[e >> 1];
+                proxy = fmaf(s_qm[wave][8 * c + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)), proxy);
+              }
+            }
+            sel = proxy > s_cut[wave];
+            if (p.dbg_proxy) p.dbg_proxy[row + j] = proxy * p.scale;
+          }
+          sel = sel || (p.local_blocks >= 0 && abs(j - qbg) <= p.local_blocks) ||
+                j < p.kv_sink_blocks || qbg < p.q_sink_blocks;
+          if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qbg) * nkb + j] != 0;
+          if (p.dbg_selected) p.dbg_selected[row + j] = sel ? 1 : 0;
+        }
+        const uint64_t bal = __ballot(sel);
+        if (lane == 0) {
+          s_mask[wave][2 * ct] = uint32_t(bal);
+          s_mask[wave][2 * ct + 1] = uint32_t(bal >> 32);
         }
       }
-    }
+      lds_barrier();
+      if (live) {
+        const uint64_t approx = tile_approx(s_mask[qg], ct, nkb);
+        if (approx) centroid_block<D>(buf, ct, approx, tk, scale_log2, qf, col, hh, st);
+      }
+    };
+    tile_stream<D, NT, R>(ring, p.NCT, RangeCursor{0},
+                          [&](int ct) { return ctiles + int64_t(ct) * S::TILE; }, process, wave, lane);
+    lds_barrier();  // every wave is done with the ring's centroid tiles
+  }
+  if (live && p.counts && lt == 0) {
+    int nsel = 0;
+    for (int w = 0; w < (nkb + 31) / 32; ++w) nsel += __builtin_popcount(s_mask[qg][w]);
+    p.counts[(int64_t(b) * p.NQB + qb) * p.H + h] = nsel;
   }
 
-  // 5. Exact blocks through the LDS ring (this wave's key half).
-  __syncthreads();  // Q staging is dead; the ring is free
-  const uint16_t* head_tiles = p.tiles + head * p.NKB * S::TILE;
-  MaskCursor cursor{s_mask, 0, s_mask[0]};
-  exact_stream<D, NT, 1>(head_tiles, ring, nsel, cursor, p.Tk, p.scale_log2, kh, qf, wave, lane, st);
+  // 4. Exact pass over the union of the group's selected blocks.
+  UnionCursor<G> cursor{&s_mask[0][0], kMaskWords, nkb};
+  const int count = cursor.count();
+  const uint32_t* my_mask = s_mask[qg];
+  const uint16_t* tiles = p.tiles + head * nkb * S::TILE;
+  tile_stream<D, NT, R>(
+      ring, count, cursor, [&](int j) { return tiles + int64_t(j) * S::TILE; },
+      [&](const uint16_t* buf, int j) {
+        if ((my_mask[j >> 5] >> (j & 31)) & 1u) exact_block<D>(buf, j, tk, scale_log2, qf, col, hh, st);
+      },
+      wave, lane);
 
-  // 6. Merge the key halves (waves 2, 3 -> waves 0, 1) and store.
-  __syncthreads();
-  float* scratch = reinterpret_cast<float*>(ring);  // [qh][value][lane], value = acc..., m, den
-  constexpr int NV = S::DT * 16 + 2;
-  if (kh == 1) {
-    float* dst = scratch + qh * NV * kWave;
-#pragma unroll
-    for (int dt = 0; dt < S::DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) dst[(dt * 16 + e) * kWave + lane] = st.acc[dt][e];
-    dst[(NV - 2) * kWave + lane] = st.m;
-    dst[(NV - 1) * kWave + lane] = st.den;
-  }
-  __syncthreads();
-  if (kh == 0) {
-    const float* src = scratch + qh * NV * kWave;
-    const float m1 = src[(NV - 2) * kWave + lane];
-    const float d1 = src[(NV - 1) * kWave + lane];
-    const float m = fmaxf(st.m, m1);
-    const float safe = m == kNegInf ? 0.f : m;
-    const float a0 = fast_exp2(st.m - safe), a1 = fast_exp2(m1 - safe);
-#pragma unroll
-    for (int dt = 0; dt < S::DT; ++dt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e)
-        st.acc[dt][e] = st.acc[dt][e] * a0 + src[(dt * 16 + e) * kWave + lane] * a1;
-    st.den = st.den * a0 + d1 * a1;
-    store_output<D>(p, b, h, q0 + myq, hh, st);
-  }
+  // 5. Normalise and store.
+  if (live) store_output<D>(p, b, h, qb * kBlock + myq, hh, st);
 }
 
 template <int D>
@@ -500,7 +614,8 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   const int h = bh % p.H, b = bh / p.H;
   const int64_t head = int64_t(b) * p.H + h;
   const int q0 = qt * QROWS;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, hh = lane >> 5;
 
   for (int idx = tid; idx < QROWS * S::DC; idx += NT) {
@@ -519,17 +634,34 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
 
   State<D> st;
   state_init(st);
-  exact_stream<D, NT, 2>(p.tiles + head * p.NKB * S::TILE, ring, p.NKB, RangeCursor{0}, p.Tk,
-                         p.scale_log2, 0, qf, wave, lane, st);
+  const int tk = p.Tk;
+  const float scale_log2 = p.scale_log2;
+  const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
+  tile_stream<D, NT, 2>(
+      ring, p.NKB, RangeCursor{0}, [&](int j) { return tiles + int64_t(j) * S::TILE; },
+      [&](const uint16_t* buf, int j) { exact_block<D>(buf, j, tk, scale_log2, qf, col, hh, st); },
+      wave, lane);
   store_output<D>(p, b, h, q0 + myq, hh, st);
 }
 
+// Query blocks per workgroup and LDS ring depth of the SOL kernel.
+#ifndef SOL_GROUP
+#define SOL_GROUP 2
+#endif
+#ifndef SOL_RING
+#define SOL_RING 2
+#endif
+constexpr int kSolGroup = SOL_GROUP;
+constexpr int kSolRing = SOL_RING;
+
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
-  const unsigned grid = xcd_grid(p.B * p.H, p.NQB);
+  const unsigned grid = xcd_grid(p.B * p.H, (p.NQB + kSolGroup - 1) / kSolGroup);
   if (D == 128)
-    hipLaunchKernelGGL(sol_attention_kernel<128>, dim3(grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((sol_attention_kernel<128, kSolGroup, kSolRing>), dim3(grid),
+                       dim3(128 * kSolGroup), 0, stream, p);
   else
-    hipLaunchKernelGGL(sol_attention_kernel<64>, dim3(grid), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((sol_attention_kernel<64, kSolGroup, kSolRing>), dim3(grid),
+                       dim3(128 * kSolGroup), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -61,16 +61,16 @@ int sol_abi_version(void) { return SOL_ABI_VERSION; }
 const char* sol_last_error(void) { return g_last_error.c_str(); }
 
 int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
-                   int64_t sizes[5]) {
+                   int64_t sizes[4]) {
   if (!sizes || !shape_ok(batch, key_tokens, heads, head_dim))
     return fail(SOL_ERR_INVALID, "sol_pool_sizes: invalid shape");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
-  const int64_t nkbp = cdiv(nkb, 32) * 32;
-  sizes[0] = batch * heads * nkb * head_dim * 2;
-  sizes[1] = batch * heads * head_dim * nkbp * 2;
+  const int64_t nct = cdiv(nkb, SOL_BLOCK);
+  const int64_t tile = 2 * SOL_BLOCK * head_dim * 2;
+  sizes[0] = batch * heads * nct * tile;
+  sizes[1] = batch * heads * nkb * tile;
   sizes[2] = batch * heads * cdiv(nkb, 16) * 2 * head_dim * 4;
   sizes[3] = batch * heads * head_dim * 4;
-  sizes[4] = batch * heads * nkb * 2 * SOL_BLOCK * head_dim * 2;
   return SOL_OK;
 }
 
@@ -78,8 +78,8 @@ namespace {
 
 int pool_checked(const char* who, const void* k, const int64_t* k_strides, const void* v,
                  const int64_t* v_strides, const int64_t* key_index, int64_t batch,
-                 int64_t key_tokens, int64_t heads, int64_t head_dim, void* kc, void* vct,
-                 void* tiles, float* chunk_sums, float* key_mean, float* key_var, void* stream) {
+                 int64_t key_tokens, int64_t heads, int64_t head_dim, void* ctiles, void* tiles,
+                 float* chunk_sums, float* key_mean, float* key_var, void* stream) {
   static thread_local std::string msg;
   auto err = [&](int code, const char* what) {
     msg = std::string(who) + ": " + what;
@@ -90,20 +90,18 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
   const bool indexed = key_index != nullptr;
   if (!operand_ok(k, k_strides, indexed) || !operand_ok(v, v_strides, indexed))
     return err(SOL_ERR_INVALID, "K/V need 16-byte aligned rows and positive strides");
-  if (bool(kc) != bool(vct)) return err(SOL_ERR_INVALID, "kc and vct go together");
-  if (!kc && !tiles) return err(SOL_ERR_INVALID, "nothing to write");
-  if ((kc && (!aligned16(kc) || !aligned16(vct))) || (tiles && !aligned16(tiles)))
-    return err(SOL_ERR_INVALID, "kc/vct/tiles must be 16-byte aligned device buffers");
+  if (!ctiles && !tiles) return err(SOL_ERR_INVALID, "nothing to write");
+  if ((ctiles && !aligned16(ctiles)) || (tiles && !aligned16(tiles)))
+    return err(SOL_ERR_INVALID, "ctiles/tiles must be 16-byte aligned device buffers");
   const bool moments = chunk_sums || key_mean || key_var;
-  if (moments && !(chunk_sums && key_mean && key_var && kc))
-    return err(SOL_ERR_INVALID, "chunk_sums, key_mean and key_var go together (with kc)");
+  if (moments && !(chunk_sums && key_mean && key_var && ctiles))
+    return err(SOL_ERR_INVALID, "chunk_sums, key_mean and key_var go together (with ctiles)");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
   if (nkb > (int64_t(1) << 19)) return err(SOL_ERR_UNSUPPORTED, "too many key blocks");
   sol::PoolParams p;
   p.k = rows_of(k, k_strides, key_index, key_tokens);
   p.v = rows_of(v, v_strides, key_index, key_tokens);
-  p.kc = static_cast<uint16_t*>(kc);
-  p.vct = static_cast<uint16_t*>(vct);
+  p.ctiles = static_cast<uint16_t*>(ctiles);
   p.tiles = static_cast<uint16_t*>(tiles);
   p.ksum = moments ? chunk_sums : nullptr;
   p.mean = key_mean;
@@ -112,8 +110,8 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
   p.H = int(heads);
   p.Tk = int(key_tokens);
   p.NKB = int(nkb);
-  p.NKBP = int(cdiv(nkb, 32) * 32);
-  p.NCHP = p.NKBP / sol::kPoolChunk;
+  p.NCT = int(cdiv(nkb, SOL_BLOCK));
+  p.NCHP = p.NCT * (SOL_BLOCK / sol::kPoolChunk);
   return hip_status(sol::launch_pool(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
@@ -121,15 +119,15 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
 
 int sol_pool_kv(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                 const int64_t* key_index, int64_t batch, int64_t key_tokens, int64_t heads,
-                int64_t head_dim, void* kc, void* vct, void* tiles, float* chunk_sums,
-                float* key_mean, float* key_var, void* stream) {
+                int64_t head_dim, void* ctiles, void* tiles, float* chunk_sums, float* key_mean,
+                float* key_var, void* stream) {
   return pool_checked("sol_pool_kv", k, k_strides, v, v_strides, key_index, batch, key_tokens,
-                      heads, head_dim, kc, vct, tiles, chunk_sums, key_mean, key_var, stream);
+                      heads, head_dim, ctiles, tiles, chunk_sums, key_mean, key_var, stream);
 }
 
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
-                      int64_t head_dim, const void* tiles, const void* kc, const void* vct,
+                      int64_t head_dim, const void* tiles, const void* ctiles,
                       const float* key_mean, const float* key_var, const uint8_t* protection,
                       double scale, double beta, int64_t local_blocks, int64_t kv_sink_tokens,
                       int64_t query_sink_tokens, void* out, int32_t* counts,
@@ -146,9 +144,8 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   if (kv_sink_tokens < 0 || query_sink_tokens < 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: sink token counts must be nonnegative");
   const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
-  if (!tiles || !kc || !vct || !aligned16(tiles) || !aligned16(kc) || !aligned16(vct) || !out ||
-      !aligned16(out))
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: tiles/kc/vct/out must be 16-byte aligned device buffers");
+  if (!tiles || !ctiles || !aligned16(tiles) || !aligned16(ctiles) || !out || !aligned16(out))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: tiles/ctiles/out must be 16-byte aligned device buffers");
   if (force == 0 && (!key_mean || !key_var))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
@@ -161,8 +158,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   std::memset(&p, 0, sizeof(p));
   p.q = rows_of(q, q_strides, query_index, query_tokens);
   p.tiles = static_cast<const uint16_t*>(tiles);
-  p.kc = static_cast<const uint16_t*>(kc);
-  p.vct = static_cast<const uint16_t*>(vct);
+  p.ctiles = static_cast<const uint16_t*>(ctiles);
   p.mean = key_mean;
   p.var = key_var;
   p.protection = protection;
@@ -177,7 +173,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   p.Tk = int(key_tokens);
   p.NQB = int(nqb);
   p.NKB = int(nkb);
-  p.NKBP = int(cdiv(nkb, 32) * 32);
+  p.NCT = int(cdiv(nkb, SOL_BLOCK));
   p.scale = float(scale);
   p.scale_log2 = float(scale * 1.4426950408889634);
   p.beta = force == 0 ? float(beta) : 0.f;
@@ -204,8 +200,8 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
   if (batch * heads * cdiv(query_tokens, 128) >= (int64_t(1) << 31))
     return fail(SOL_ERR_UNSUPPORTED, "sol_dense_fwd: grid too large");
   const int rc = pool_checked("sol_dense_fwd", k, k_strides, v, v_strides, nullptr, batch,
-                              key_tokens, heads, head_dim, nullptr, nullptr, tiles, nullptr,
-                              nullptr, nullptr, stream);
+                              key_tokens, heads, head_dim, nullptr, tiles, nullptr, nullptr,
+                              nullptr, stream);
   if (rc != SOL_OK) return rc;
   sol::AttnParams p;
   std::memset(&p, 0, sizeof(p));

@@ -4,11 +4,11 @@
 // 185-190) and `_moments` (kernels.py:30-49).  HBM-bound: every K and V token
 // row is read exactly once with 16-byte loads (through the index for indexed
 // windows); the outputs are written in the layouts the attention kernels use:
-//   KC    [B, H, NKB, D]   bf16, one contiguous row per key block
-//   VCt   [B, H, D, NKBP]  bf16, key blocks contiguous per feature (NKBP = NKB
-//                          rounded up to 32, zero padded) -> MFMA A operand
-//   tiles [B, H, NKB, 2, 64 D] swizzled K and V^T block tiles (TileLayout),
-//                          streamed by the exact-block loop with LDS DMA
+//   ctiles [B, H, NCT, 2, 64 D] BF16 block centroids, 64 key blocks per tile,
+//                          as a swizzled K / V^T tile pair (TileLayout);
+//                          NCT = ceil(NKB / 64), zero beyond the last block
+//   tiles  [B, H, NKB, 2, 64 D] swizzled K and V^T token tiles per key block
+// Both are streamed into LDS by the attention kernels with DMA.
 // Sums follow torch's CPU outer-reduction order (16-row sequential chunks,
 // folded in order), so the FP32 means and the BF16-rounded centroids equal the
 // reference oracle's `x[:, i:i+64].float().mean(1)` bit for bit.
@@ -116,14 +116,17 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
   __syncthreads();
 
   const int64_t head = int64_t(b) * p.H + h;
-  if (!p.kc) return;  // tiles only (dense path)
+  if (!p.ctiles) return;  // tiles only (dense path)
+  // Centroid tiles: 64 consecutive key blocks per tile, laid out like a K / V^T
+  // tile pair.  This chunk fills rows r0 .. r0 + 15 of tile ct.
+  const int ct = (c * kPoolChunk) / kBlock;
+  const int r0 = (c * kPoolChunk) % kBlock;
+  uint16_t* ctile = p.ctiles + (head * p.NCT + ct) * 2 * TL::kElems;
   if (!is_v) {
     if (tid < kPoolChunk * DC) {
       const int jb = tid / DC, cc = tid % DC;
-      const int j = c * kPoolChunk + jb;
-      if (j < p.NKB)
-        *reinterpret_cast<u32x4*>(p.kc + (head * p.NKB + j) * D + 8 * cc) =
-            *reinterpret_cast<const u32x4*>(&cent[jb][8 * cc]);
+      *reinterpret_cast<u32x4*>(ctile + TL::k_offset(r0 + jb, cc)) =
+          *reinterpret_cast<const u32x4*>(&cent[jb][8 * cc]);
     }
     // Chunk partial sums of the BF16 centroids and their squares (moments).
     const int nch = (p.NKB + kPoolChunk - 1) / kPoolChunk;
@@ -139,13 +142,13 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
       dst[tid] = s1;
       dst[D + tid] = s2;
     }
-  } else if (tid < 2 * D) {
-    const int d = tid >> 1, half = tid & 1;
-    u32x4 o;
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      o[e] = uint32_t(cent[8 * half + 2 * e][d]) | (uint32_t(cent[8 * half + 2 * e + 1][d]) << 16);
-    *reinterpret_cast<u32x4*>(p.vct + (head * D + d) * p.NKBP + c * kPoolChunk + 8 * half) = o;
+  } else {
+    for (int idx = tid; idx < 4 * D; idx += 256) {
+      const int d = idx >> 2, gq = idx & 3;  // 4-centroid group gq of this chunk
+      const u32x2 o = {uint32_t(cent[4 * gq][d]) | (uint32_t(cent[4 * gq + 1][d]) << 16),
+                       uint32_t(cent[4 * gq + 2][d]) | (uint32_t(cent[4 * gq + 3][d]) << 16)};
+      *reinterpret_cast<u32x2*>(ctile + TL::kElems + TL::vt_offset(d, r0 / 4 + gq)) = o;
+    }
   }
 }
 
@@ -223,7 +226,7 @@ hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
   else
     hipLaunchKernelGGL(pool_kv_kernel<64>, grid, dim3(256), 0, stream, p);
   hipError_t err = hipGetLastError();
-  if (err != hipSuccess || !p.ksum || !p.kc) return err;
+  if (err != hipSuccess || !p.ksum || !p.ctiles) return err;
   if (D == 128)
     hipLaunchKernelGGL(moments_kernel<128>, dim3(p.B * p.H), dim3(kMomentThreads), 0, stream,
                        p.ksum, p.mean, p.var, p.NKB);

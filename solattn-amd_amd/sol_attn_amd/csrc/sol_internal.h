@@ -10,20 +10,18 @@ namespace sol {
 
 struct PoolParams {
   TokenRows k, v;
-  uint16_t* kc;     // [B, H, NKB, D] or null (no centroids)
-  uint16_t* vct;    // [B, H, D, NKBP] or null
-  uint16_t* tiles;  // [B, H, NKB, 2, 64 * D] swizzled K / V^T block tiles, or null
-  float* ksum;      // [B, H, NCH, 2, D] chunk sums, null -> no moments
-  float* mean;      // [B, H, D]
-  float* var;       // [B, H, D]
-  int B, H, Tk, NKB, NKBP, NCHP;
+  uint16_t* ctiles;  // [B, H, NCT, 2, 64 * D] centroid tiles, or null (tiles only)
+  uint16_t* tiles;   // [B, H, NKB, 2, 64 * D] swizzled K / V^T block tiles, or null
+  float* ksum;       // [B, H, NCH, 2, D] chunk sums, null -> no moments
+  float* mean;       // [B, H, D]
+  float* var;        // [B, H, D]
+  int B, H, Tk, NKB, NCT, NCHP;  // NCHP = 4 * NCT pooling chunks of 16 blocks
 };
 
 struct AttnParams {
   TokenRows q;
   const uint16_t* tiles;       // [B, H, NKB, 2, 64 * D] from the pooling pass
-  const uint16_t* kc;          // [B, H, NKB, D]
-  const uint16_t* vct;         // [B, H, D, NKBP]
+  const uint16_t* ctiles;      // [B, H, NCT, 2, 64 * D] centroid tiles
   const float* mean;           // [B, H, D]
   const float* var;            // [B, H, D]
   const uint8_t* protection;   // [B, NQB, NKB] or null
@@ -32,7 +30,7 @@ struct AttnParams {
   uint8_t* dbg_selected;       // [B, NQB, H, NKB] or null
   float* dbg_proxy;            // [B, NQB, H, NKB] or null
   float* dbg_cutoff;           // [B, NQB, H] or null
-  int B, H, Tq, Tk, NQB, NKB, NKBP;
+  int B, H, Tq, Tk, NQB, NKB, NCT;
   float scale, scale_log2, beta;
   int force;          // 0 finite beta, 1 beta = -inf (all exact), 2 beta = +inf
   int local_blocks;   // < 0 disables the local band

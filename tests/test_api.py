@@ -128,10 +128,10 @@ def test_c_abi_library_exports_every_declared_symbol():
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
     assert native.sol_abi_version() == 1
-    sizes = (ctypes.c_int64 * 5)()
+    sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
-    assert list(sizes) == [1 * 2 * 5 * 64 * 2, 1 * 2 * 64 * 32 * 2, 1 * 2 * 1 * 2 * 64 * 4, 2 * 64 * 4,
-                           1 * 2 * 5 * 2 * 64 * 64 * 2]
+    tile = 2 * 64 * 64 * 2
+    assert list(sizes) == [1 * 2 * 1 * tile, 1 * 2 * 5 * tile, 1 * 2 * 1 * 2 * 64 * 4, 2 * 64 * 4]
     assert native.sol_pool_sizes(1, 317, 2, 96, sizes) == -1
     assert b"invalid shape" in native.sol_last_error()
 
@@ -145,14 +145,14 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     rc = native.sol_dense_fwd(fake, strides, fake, strides, fake, strides, 1, 193, 317, 2, 64,
                               float("nan"), fake, fake, None)
     assert rc == -1 and b"scale" in native.sol_last_error()
-    rc = native.sol_attention_fwd(fake, strides, None, 1, 193, 317, 2, 64, fake, fake, fake,
+    rc = native.sol_attention_fwd(fake, strides, None, 1, 193, 317, 2, 64, fake, fake,
                                   None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None,
                                   None, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
     bad = (ctypes.c_int64 * 3)(64 * 2 * 317, 127, 64)
-    rc = native.sol_pool_kv(fake, bad, fake, strides, None, 1, 317, 2, 64, fake, fake, fake,
+    rc = native.sol_pool_kv(fake, bad, fake, strides, None, 1, 317, 2, 64, fake, fake,
                             None, None, None, None)
     assert rc == -1 and b"aligned" in native.sol_last_error()
-    rc = native.sol_pool_kv(fake, strides, fake, strides, None, 1, 317, 2, 64, None, None, None,
+    rc = native.sol_pool_kv(fake, strides, fake, strides, None, 1, 317, 2, 64, None, None,
                             None, None, None, None)
     assert rc == -1 and b"nothing to write" in native.sol_last_error()

@@ -28,28 +28,46 @@ def kernel_pool(k, v, moments=True):
         return _native.pool_kv(k, v, moments=moments)
 
 
-def check_tiles(tiles, k, v):
-    """Un-swizzle the attention tiles on the CPU and compare with K / V^T blocks."""
-    t = tiles.cpu().view(torch.int16).numpy().view(np.uint16)   # [B, H, NKB, 2, 64 D]
-    kb = k.contiguous().view(torch.int16).numpy().view(np.uint16)
-    vb = v.contiguous().view(torch.int16).numpy().view(np.uint16)
-    b, h, nkb, _, e = t.shape
+def unswizzle(tiles):
+    """Tile pairs ``[B, H, N, 2, 64 D]`` -> K rows ``[B, H, N, 64, D]`` and
+    V^T rows ``[B, H, N, D, 64]`` (uint16 BF16 bits), undoing the bank swizzle."""
+    t = tiles.cpu().view(torch.int16).numpy().view(np.uint16)
+    b, h, n, _, e = t.shape
     d = e // 64
-    tk = kb.shape[1]
-    pad = nkb * 64 - tk
-    kp = np.concatenate([kb, np.zeros((b, pad) + kb.shape[2:], np.uint16)], 1)
-    vp = np.concatenate([vb, np.zeros((b, pad) + vb.shape[2:], np.uint16)], 1)
-    kt = t[:, :, :, 0].reshape(b, h, nkb, 64, d // 8, 8)
+    kt = t[:, :, :, 0].reshape(b, h, n, 64, d // 8, 8)
     rows = np.arange(64)[:, None]
     chunks = np.arange(d // 8)[None, :]
     swz = (rows & 15) if d == 128 else ((rows >> 1) & 7)
-    k_unswz = kt[:, :, :, rows, chunks ^ swz].reshape(b, h, nkb, 64, d)
-    np.testing.assert_array_equal(k_unswz, kp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 2, 4))
-    vt = t[:, :, :, 1].reshape(b, h, nkb, d, 16, 4)
+    k_rows = kt[:, :, :, rows, chunks ^ swz].reshape(b, h, n, 64, d)
+    vt = t[:, :, :, 1].reshape(b, h, n, d, 16, 4)
     dd = np.arange(d)[:, None]
     groups = np.arange(16)[None, :]
-    v_unswz = vt[:, :, :, dd, groups ^ (dd & 15) ^ ((dd >> 4) & 1)].reshape(b, h, nkb, d, 64)
-    np.testing.assert_array_equal(v_unswz, vp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 4, 2))
+    v_rows = vt[:, :, :, dd, groups ^ (dd & 15) ^ ((dd >> 4) & 1)].reshape(b, h, n, d, 64)
+    return k_rows, v_rows
+
+
+def check_tiles(tiles, k, v):
+    """The attention tiles hold K / V^T of every key block, zero past the end."""
+    kb = k.contiguous().view(torch.int16).numpy().view(np.uint16)
+    vb = v.contiguous().view(torch.int16).numpy().view(np.uint16)
+    k_rows, v_rows = unswizzle(tiles)
+    b, h, nkb, d = k_rows.shape[0], k_rows.shape[1], k_rows.shape[2], k_rows.shape[4]
+    pad = nkb * 64 - kb.shape[1]
+    kp = np.concatenate([kb, np.zeros((b, pad) + kb.shape[2:], np.uint16)], 1)
+    vp = np.concatenate([vb, np.zeros((b, pad) + vb.shape[2:], np.uint16)], 1)
+    np.testing.assert_array_equal(k_rows, kp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 2, 4))
+    np.testing.assert_array_equal(v_rows, vp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 4, 2))
+
+
+def centroids(ctiles, nkb):
+    """Centroid tiles -> K and V block centroids ``[B, NKB, H, D]`` float32 (+ padding check)."""
+    k_rows, v_rows = unswizzle(ctiles)              # [B, H, NCT, 64, D], [B, H, NCT, D, 64]
+    b, h, nct, _, d = k_rows.shape
+    kc = k_rows.reshape(b, h, nct * 64, d)
+    vc = v_rows.transpose(0, 1, 2, 4, 3).reshape(b, h, nct * 64, d)
+    assert (kc[:, :, nkb:] == 0).all() and (vc[:, :, nkb:] == 0).all()
+    f = lambda x: orc.bf16_bits_to_f32(x[:, :, :nkb]).transpose(0, 2, 1, 3)
+    return f(kc), f(vc)
 
 
 @pytest.mark.parametrize("shape", [(1, 317, 2, 64), (2, 1089, 3, 128), (1, 1, 1, 64), (2, 4096, 16, 128),
@@ -65,11 +83,9 @@ def test_pooling_and_moments_bit_exact(shape):
     kc = orc.block_means(to_np(k), True)          # [B, NKB, H, D]
     vc = orc.block_means(to_np(v), True)
     mean, var = orc.key_moments(kc)
-    nkb = kc.shape[1]
-    np.testing.assert_array_equal(to_np(out["kc"]).transpose(0, 2, 1, 3), kc)
-    vct = to_np(out["vct"])
-    np.testing.assert_array_equal(vct[..., :nkb].transpose(0, 3, 1, 2), vc)
-    assert (vct[..., nkb:] == 0).all()
+    got_kc, got_vc = centroids(out["ctiles"], kc.shape[1])
+    np.testing.assert_array_equal(got_kc, kc)
+    np.testing.assert_array_equal(got_vc, vc)
     np.testing.assert_array_equal(to_np(out["mean"]), mean)
     np.testing.assert_array_equal(to_np(out["var"]), var)
 
@@ -84,8 +100,9 @@ def test_pooling_strided_and_indexed_gather():
     check_tiles(out["tiles"], k.cpu()[keys], v.cpu()[keys])
     kc = orc.block_means(to_np(k.cpu()[keys]), True)
     vc = orc.block_means(to_np(v.cpu()[keys]), True)
-    np.testing.assert_array_equal(to_np(out["kc"]).transpose(0, 2, 1, 3), kc)
-    np.testing.assert_array_equal(to_np(out["vct"])[..., :kc.shape[1]].transpose(0, 3, 1, 2), vc)
+    got_kc, got_vc = centroids(out["ctiles"], kc.shape[1])
+    np.testing.assert_array_equal(got_kc, kc)
+    np.testing.assert_array_equal(got_vc, vc)
     mean, var = orc.key_moments(kc)
     np.testing.assert_array_equal(to_np(out["mean"]), mean)
     np.testing.assert_array_equal(to_np(out["var"]), var)
