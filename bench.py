@@ -99,6 +99,22 @@ def routing_flops(selected, tq, tk, d):
     return exact, approx
 
 
+def measured_traffic(workload):
+    """Memory-side bytes per launch of the SOL kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of this workload (None if there is none)."""
+    path = os.path.join(ROOT, "profiles", f"sol_attention_{workload}_hbm_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("TRAFFIC_JSON "):
+                    rec = json.loads(line[len("TRAFFIC_JSON "):])
+                    rec["source"] = os.path.relpath(path, ROOT)
+                    return rec
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(q, k, v, cfg, scale, sample, gpu_out, gpu_sel):
     """The oracle on `sample` query blocks x all heads, timed on host cores."""
     from oracle import sol_oracle as orc
@@ -205,6 +221,7 @@ def main():
     pool_bytes = 2 * b * t * h * d * 2 + (pooled["ctiles"].numel() + pooled["tiles"].numel()) * 2
     pool_gbs = pool_bytes / (pool_ms * 1e-3) / 1e9
 
+    traffic = measured_traffic(args.workload)
     result = {
         "metric": "ms/call & dense-equiv TFLOP/s at 84,672 tok H24 D128 BF16; density; err vs oracle",
         "value": dense_flops / (wall_ms * 1e-3) / 1e12,
@@ -224,7 +241,11 @@ def main():
         "dense_hip_tflops": dense_flops / (dense_ms * 1e-3) / 1e12,
         "speedup_vs_dense_hip": dense_ms / wall_ms,
         "roofline": {"bound": "mfma", "achieved": attn_tflops, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": attn_tflops / PEAK_BF16_TFLOPS, "traffic": None,
+                     "unit": "TFLOP/s", "frac": attn_tflops / PEAK_BF16_TFLOPS,
+                     "traffic": traffic["traffic_bytes"] if traffic else None,
+                     "traffic_source": (f"{traffic['source']} ({traffic['kernel']}: rocprofv3 FETCH_SIZE x "
+                                        f"{traffic['fetch_scale']} + WRITE_SIZE x {traffic['write_scale']}, "
+                                        f"scaled by a 1 GiB copy)") if traffic else None,
                      "kernel": "sol attention (routing + centroid correction + exact blocks)",
                      "flops_per_launch": exact_flops + approx_flops, "exact_flops": exact_flops,
                      "exact_only_frac": exact_flops / (attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
