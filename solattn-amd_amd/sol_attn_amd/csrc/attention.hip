@@ -96,42 +96,11 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
 
-// Online-softmax update with raw scores s[0..NS) (-inf = absent).  Scores are
-// scaled to log2 units inside the exponent: p = exp2(s * c - m), m the running
-// max in log2 units.  Each p is multiplied by weight(t, e) (centroid tiles:
-// the block's valid length).  Returns the probabilities in s.  The
-// accumulator rescale is skipped when no query of the wave raised its max.
+// Per-element weight on exp2(s c - m): 1 for exact tokens, the block's valid
+// length for centroids.
 struct UnitWeight {
   __device__ __forceinline__ float operator()(int, int) const { return 1.f; }
 };
-
-template <int D, int NS, typename Weight>
-__device__ __forceinline__ void softmax_update(State<D>& st, f32x16 (&s)[NS], float c, Weight weight) {
-  float mx = kNegInf;
-#pragma unroll
-  for (int t = 0; t < NS; ++t)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
-  mx = pair_max(mx) * c;
-  const float mnew = fmaxf(st.m, mx);
-  const float safe = mnew == kNegInf ? 0.f : mnew;
-  const float alpha = fast_exp2(st.m - safe);
-  float lsum = 0.f;
-#pragma unroll
-  for (int t = 0; t < NS; ++t)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float pe = fast_exp2(fmaf(s[t][e], c, -safe)) * weight(t, e);
-      s[t][e] = pe;
-      lsum += pe;
-    }
-  st.den = st.den * alpha + lsum;
-  st.m = mnew;
-  if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-    for (int dt = 0; dt < Shape<D>::DT; ++dt) st.acc[dt] *= alpha;
-  }
-}
 
 __device__ __forceinline__ bf16x8 pack8(const f32x16& s, int base) {
   u32x4 pb;
@@ -140,22 +109,32 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& s, int base) {
   return as_bf16x8(pb);
 }
 
-// 16-byte global -> LDS DMA per lane: lane l's bytes land at lds_base + 16 l.
-// Issued as inline assembly so that the compiler does not drain the vector
-// memory counter before every LDS read (it cannot tell the ring's buffers
-// apart); completion is awaited explicitly with wait_vmcnt before the barrier.
-// M0 (the LDS base register of the DMA) is saved and restored around it.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds_base) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);  // wave-uniform by construction
+// 16-byte global -> LDS DMA per lane: lane l reads base + lane_bytes and its
+// bytes land at lds_base + 16 l.  The wave-uniform base travels in an SGPR
+// pair (global "saddr" form) and the per-lane part is a 32-bit offset, so a
+// refill holds no 64-bit per-lane addresses in vector registers.  Issued as
+// inline assembly so that the compiler does not drain the vector memory
+// counter before every LDS read (it cannot tell the ring's buffers apart);
+// completion is awaited explicitly with wait_vmcnt before the barrier.  M0
+// (the LDS base register of the DMA) is saved and restored around it.
+__device__ __forceinline__ void dma16(const uint16_t* base, uint32_t lane_bytes, uint32_t lds_base) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  // Wave-uniform by construction; readfirstlane makes that visible to the
+  // compiler.  It returns a signed int: each half goes through uint32_t so
+  // that the low word is zero-extended, never sign-extended into the high word.
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(b)));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(b >> 32)));
+  const uint64_t sbase = (uint64_t(hi) << 32) | uint64_t(lo);
+  const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(lds_base));
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
       "s_mov_b32 m0, %1\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %2, off\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "s"(base), "v"(src)
+      : "s"(m), "v"(lane_bytes), "s"(sbase)
       : "memory");
 }
 
@@ -163,17 +142,41 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
   return uint32_t(reinterpret_cast<uintptr_t>((SOL_LDS const void*)p));
 }
 
-// Issue the DMA of one K + V^T tile pair (contiguous in HBM) into an LDS buffer.
+// DMA of one K + V^T tile pair (contiguous in HBM) into an LDS buffer, in
+// kRounds rounds of one 16-byte chunk per lane.  A refill can be issued
+// whole, or a few rounds at a time between a wave's score MFMAs, so that
+// the wave's in-order instruction stream does not stall on a burst of DMA
+// issues.  Every round must be issued exactly once per refill.
+template <int D, int NT>
+struct TileRefill {
+  static constexpr int kChunks = Shape<D>::TILE / 8;  // 16-byte chunks per tile pair
+  static constexpr int kRounds = kChunks / NT;
+  static_assert(kChunks % NT == 0, "tile pair must split evenly over the workgroup");
+  const uint16_t* src;  // nullptr: nothing to load
+  uint16_t* dst;
+  int wave, lane;
+
+  __device__ __forceinline__ void round(int r) const {
+    if (src) {
+      const int chunk = r * NT + wave * kWave;  // first chunk of this wave's 1 KB piece
+      dma16(src + chunk * 8, uint32_t(lane) * 16u, lds_address(dst + chunk * 8));
+    }
+  }
+  __device__ __forceinline__ void all() const {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) round(r);
+  }
+  // The rounds that belong after k-step ks of a KT-step score loop.
+  template <int KT>
+  __device__ __forceinline__ void after_kstep(int ks) const {
+#pragma unroll
+    for (int r = ks * kRounds / KT; r < (ks + 1) * kRounds / KT; ++r) round(r);
+  }
+};
+
 template <int D, int NT>
 __device__ __forceinline__ void tile_dma(const uint16_t* src, uint16_t* dst, int wave, int lane) {
-  constexpr int kChunks = Shape<D>::TILE / 8;   // 16-byte chunks per tile pair
-  constexpr int kRounds = kChunks / NT;
-  static_assert(kChunks % NT == 0, "tile pair must split evenly over the workgroup");
-#pragma unroll
-  for (int r = 0; r < kRounds; ++r) {
-    const int chunk = r * NT + wave * kWave;  // first chunk of this wave's 1 KB piece
-    dma16(src + (chunk + lane) * 8, lds_address(dst + chunk * 8));
-  }
+  TileRefill<D, NT>{src, dst, wave, lane}.all();
 }
 
 template <int N>
@@ -200,10 +203,11 @@ __device__ __forceinline__ int fresh(int x) {
 // fragments are read and multiplied first; the V^T fragments are read after
 // the last score MFMA has issued (a scheduling barrier keeps them there), so
 // they reuse the K fragments' registers and arrive during the softmax.
-template <int D, int NH>
+template <int D, int NH, typename Refill>
 __device__ __forceinline__ void tile_scores(const uint16_t* buf, int kh0,
                                             const bf16x8 (&qf)[Shape<D>::KT], int col, int hh,
-                                            f32x16 (&p)[NH], u32x4 (&va)[NH][2][Shape<D>::DT]) {
+                                            f32x16 (&p)[NH], u32x4 (&va)[NH][2][Shape<D>::DT],
+                                            const Refill& refill) {
   using S = Shape<D>;
   using TL = TileLayout<D>;
   const uint16_t* kt_lds = buf;
@@ -219,9 +223,11 @@ __device__ __forceinline__ void tile_scores(const uint16_t* buf, int kh0,
 #pragma unroll
   for (int t = 0; t < NH; ++t) p[t] = zero16();
 #pragma unroll
-  for (int ks = 0; ks < S::KT; ++ks)
+  for (int ks = 0; ks < S::KT; ++ks) {
 #pragma unroll
     for (int t = 0; t < NH; ++t) p[t] = mfma32x32x16(as_bf16x8(ka[t][ks]), qf[ks], p[t]);
+    refill.template after_kstep<S::KT>(ks);
+  }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int t = 0; t < NH; ++t)
@@ -238,19 +244,59 @@ __device__ __forceinline__ void tile_scores(const uint16_t* buf, int kh0,
     }
 }
 
-// O^T += V^T * bf16(P)^T for key halves [kh0, kh0 + NH).
-template <int D, int NH>
-__device__ __forceinline__ void tile_pv(const f32x16 (&p)[NH], const u32x4 (&va)[NH][2][Shape<D>::DT],
-                                        State<D>& st) {
+// Lazy online softmax + P V for one 64-key tile (two 32-key halves) of raw
+// scores s (-inf = absent); c = scale * log2(e) moves them to log2 units
+// inside the exponent.  The wave's running max m (log2 units) moves only when
+// some query's tile max exceeds it by more than kRescaleSlack; otherwise the
+// tile's probabilities exp2(s c - m) * weight may exceed 1 by up to
+// 2^kRescaleSlack (times the weight), which FP32 sums and BF16 products carry
+// at unchanged relative precision.  acc and den always share m, so
+// O = acc / den is unaffected.  Without a rescale the second half's exp2 work
+// does not depend on the first half's P V products, and the schedule
+// interleaves the two (one MFMA, then VALU work, repeated).
+constexpr float kRescaleSlack = 8.f;
+
+template <int D, typename Weight>
+__device__ __forceinline__ void softmax_pv(State<D>& st, f32x16 (&s)[2],
+                                           const u32x4 (&va)[2][2][Shape<D>::DT], float c,
+                                           Weight weight) {
+  constexpr int DT = Shape<D>::DT;
+  float mx = kNegInf;
 #pragma unroll
-  for (int t = 0; t < NH; ++t)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const bf16x8 b = pack8(p[t], 8 * c);
+    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
+  mx = pair_max(mx) * c;
+  if (__builtin_amdgcn_ballot_w64(mx > st.m + kRescaleSlack)) {
+    const float mnew = fmaxf(st.m, mx);
+    const float alpha = fast_exp2(st.m - (mnew == kNegInf ? 0.f : mnew));
+    st.den *= alpha;
 #pragma unroll
-      for (int dt = 0; dt < Shape<D>::DT; ++dt)
-        st.acc[dt] = mfma32x32x16(as_bf16x8(va[t][c][dt]), b, st.acc[dt]);
+    for (int dt = 0; dt < DT; ++dt) st.acc[dt] *= alpha;
+    st.m = mnew;
+  }
+  const float neg_m = st.m == kNegInf ? 0.f : -st.m;
+  float lsum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pe = fast_exp2(fmaf(s[t][e], c, neg_m)) * weight(t, e);
+      s[t][e] = pe;
+      lsum += pe;
     }
+    const bf16x8 b0 = pack8(s[t], 0), b1 = pack8(s[t], 8);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) st.acc[dt] = mfma32x32x16(as_bf16x8(va[t][0][dt]), b0, st.acc[dt]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) st.acc[dt] = mfma32x32x16(as_bf16x8(va[t][1][dt]), b1, st.acc[dt]);
+  }
+  st.den += lsum;
+#pragma unroll
+  for (int i = 0; i < 2 * DT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // then up to six VALU
+  }
 }
 
 // Key row (inside a 64-row tile) of element e of this lane's 32-key half t.
@@ -258,35 +304,34 @@ __device__ __forceinline__ int tile_row(int t, int e, int hh) {
   return 32 * t + 8 * (e >> 2) + 4 * hh + (e & 3);
 }
 
-// Exact 64-key block j from an LDS tile pair (both key halves).
+// What a wave carries from the LDS phase of a tile (score MFMAs issued,
+// V^T fragments read) to its compute phase.
 template <int D>
-__device__ __forceinline__ void exact_block(const uint16_t* buf, int j, int tk, float scale_log2,
-                                            const bf16x8 (&qf)[Shape<D>::KT], int col, int hh,
-                                            State<D>& st) {
-  f32x16 p[2];
-  u32x4 va[2][2][Shape<D>::DT];
-  tile_scores<D, 2>(buf, 0, qf, col, hh, p, va);
+struct TileFrags {
+  f32x16 p[2];                   // raw scores of the two 32-key halves
+  u32x4 va[2][2][Shape<D>::DT];  // V^T fragments
+};
+
+// Exact 64-key block j: tail mask, online softmax, P V.
+template <int D>
+__device__ __forceinline__ void exact_finish(TileFrags<D>& f, int j, int tk, float scale_log2, int hh,
+                                             State<D>& st) {
   if ((j + 1) * kBlock > tk) {  // tail block: keys past the end are absent
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int e = 0; e < 16; ++e)
-        if (j * kBlock + tile_row(t, e, hh) >= tk) p[t][e] = kNegInf;
+        if (j * kBlock + tile_row(t, e, hh) >= tk) f.p[t][e] = kNegInf;
   }
-  softmax_update<D, 2>(st, p, scale_log2, UnitWeight{});
-  tile_pv<D, 2>(p, va, st);
+  softmax_pv<D>(st, f.p, f.va, scale_log2, UnitWeight{});
 }
 
 // Centroid tile ct: the block centroids 64 ct + r whose bit r is set in
 // `approx` contribute logit q . Kc_j + ln(len_j) and value Vc_j; the length
 // enters as a weight on exp2(s - m).
 template <int D>
-__device__ __forceinline__ void centroid_block(const uint16_t* buf, int ct, uint64_t approx, int tk,
-                                               float scale_log2, const bf16x8 (&qf)[Shape<D>::KT],
-                                               int col, int hh, State<D>& st) {
-  f32x16 p[2];
-  u32x4 va[2][2][Shape<D>::DT];
-  tile_scores<D, 2>(buf, 0, qf, col, hh, p, va);
+__device__ __forceinline__ void centroid_finish(TileFrags<D>& f, int ct, uint64_t approx, int tk,
+                                                float scale_log2, int hh, State<D>& st) {
   // Row of element e of half t = 4 hh + (a compile-time constant): only the
   // lane's share is formed at run time, so nothing per element stays live.
   const uint64_t lane_approx = approx >> (4 * hh);
@@ -295,10 +340,9 @@ __device__ __forceinline__ void centroid_block(const uint16_t* buf, int ct, uint
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int e = 0; e < 16; ++e)
-      if (!((lane_approx >> tile_row(t, e, 0)) & 1u)) p[t][e] = kNegInf;
+      if (!((lane_approx >> tile_row(t, e, 0)) & 1u)) f.p[t][e] = kNegInf;
   auto len = [&](int t, int e) { return float(min(kBlock, lane_tokens - kBlock * tile_row(t, e, 0))); };
-  softmax_update<D, 2>(st, p, scale_log2, len);
-  tile_pv<D, 2>(p, va, st);
+  softmax_pv<D>(st, f.p, f.va, scale_log2, len);
 }
 
 template <int D>
@@ -319,32 +363,44 @@ __device__ __forceinline__ void store_output(const AttnParams& p, int b, int h, 
     }
 }
 
-// Waits until at most `ahead` tiles' DMA (newest first) are still in flight.
-template <int R, int kRounds>
+// Waits until at most `ahead` tiles' DMA (the newest ones) are still in flight.
+template <int kRounds>
 __device__ __forceinline__ void wait_ahead(int ahead) {
-  static_assert(R >= 2 && R <= 4, "ring depth 2..4");
-  if (R > 3 && ahead >= 2) {
+  if (ahead >= 3) {
+    wait_vmcnt<3 * kRounds>();
+  } else if (ahead == 2) {
     wait_vmcnt<2 * kRounds>();
-  } else if (R > 2 && ahead >= 1) {
+  } else if (ahead == 1) {
     wait_vmcnt<kRounds>();
   } else {
     wait_vmcnt<0>();
   }
 }
 
+// Barrier that publishes this workgroup's LDS accesses (no global-memory
+// fence, so the ring's DMA in flight is not drained).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Streams `count` tiles through an R-slot LDS ring: while tile i is on the
 // matrix cores, the DMA of tiles i+1 .. i+R-1 is in flight.  One barrier per
 // tile: after it, tile i is visible to every wave and every wave has finished
-// tile i-1, whose slot then receives tile i+R-1.  `next()` yields tile ids in
+// tile i-1, whose slot then receives tile i+R-1.  Per tile,
+// load(buf, id, refill) reads this wave's fragments from LDS, issues the score
+// MFMAs and, between them, the rounds of that refill DMA (or all of them at
+// once when it has no scores to compute); compute(frags, id) finishes the
+// tile from registers.  `next()` yields tile ids in
 // order and is evaluated identically by every thread; source(id) is the
-// tile's HBM address; process(buf, id) consumes it.  Two streams over the
-// same ring are separated by a barrier.
-template <int D, int NT, int R, typename Next, typename Source, typename Process>
+// tile's HBM address.  Two streams over the same ring are separated by a
+// barrier.
+template <int D, int NT, int R, typename Next, typename Source, typename Load, typename Compute>
 __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next, Source source,
-                                            Process process, int wave, int lane) {
+                                            Load load, Compute compute, int wave, int lane) {
   using S = Shape<D>;
   constexpr int kRounds = S::TILE / 8 / NT;
-  static_assert((R & (R - 1)) == 0, "ring depth must be a power of two");
+  static_assert(R >= 2 && R <= 4 && (R & (R - 1)) == 0, "ring depth 2 or 4");
+  static_assert((R - 2) * kRounds <= 63, "vmcnt range");
   if (count <= 0) return;
   int ids[R - 1];  // tiles i .. i+R-2 (uniform); shifted each iteration
 #pragma unroll
@@ -353,24 +409,20 @@ __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next
     if (s < count) tile_dma<D, NT>(source(ids[s]), ring + s * S::TILE, wave, lane);
   }
   for (int i = 0; i < count; ++i) {
-    wait_ahead<R, kRounds>(min(R - 2, count - 1 - i));
+    wait_ahead<kRounds>(min(R - 2, count - 1 - i));
     ring_barrier();
     const int id = ids[0];
 #pragma unroll
     for (int s = 0; s < R - 2; ++s) ids[s] = ids[s + 1];
+    TileRefill<D, NT> refill{nullptr, ring + ((i + R - 1) & (R - 1)) * S::TILE, wave, lane};
     if (i + R - 1 < count) {
       const int idn = next();
       ids[R - 2] = idn;
-      tile_dma<D, NT>(source(idn), ring + ((i + R - 1) & (R - 1)) * S::TILE, wave, lane);
+      refill.src = source(idn);
     }
-    process(ring + (i & (R - 1)) * S::TILE, id);
+    auto frags = load(ring + (i & (R - 1)) * S::TILE, id, refill);
+    compute(frags, id);
   }
-}
-
-// Barrier that publishes this workgroup's LDS writes (no global-memory fence,
-// so the ring's DMA in flight is not drained).
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // Approximated blocks of centroid tile ct for one query block: valid blocks
@@ -529,50 +581,61 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
       for (int j = lt; j < nkb; j += 128) p.dbg_selected[dbg_row + j] = 1;
     __syncthreads();
   } else {
-    // 3. Centroid pass: routing of each tile's 64 blocks (wave g routes query
-    // block qb0 + g), then the approximated blocks' contributions.
+    // 3. Centroid pass.  Load phase: routing of the tile's 64 blocks for every
+    // query block of the group -- wave w scores blocks 32 (w & 1) + (lane & 31)
+    // of query block w >> 1 over feature half lane >> 5, the halves summed
+    // across the lane pair -- into the LDS bitmask, and this wave's centroid
+    // scores.  Compute phase (after the barrier publishes the mask): the
+    // approximated blocks' contributions.
     const uint16_t* ctiles = p.ctiles + head * p.NCT * S::TILE;
-    auto process = [&](const uint16_t* buf, int ct) {
-      if (wave < G) {
-        const int qbg = qb0 + wave;
-        const int j = kBlock * ct + lane;
-        bool sel = false;
-        if (qbg < p.NQB && j < nkb) {
-          const int64_t row = ((int64_t(b) * p.NQB + qbg) * p.H + h) * nkb;
-          if (p.force == 0) {
-            const int row_lane = fresh(lane);
-            float proxy = 0.f;
+    auto load = [&](const uint16_t* buf, int ct, const TileRefill<D, NT>& refill) {
+      const int r = fresh(32 * qh + col);  // centroid row inside the tile
+      const int j = kBlock * ct + r;
+      bool sel = false;
+      if (live && j < nkb) {
+        if (p.force == 0) {
+          const int c0 = fresh(hh) * (S::DC / 2);  // first 16-byte chunk of this lane's feature half
+          float part[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int c = 0; c < S::DC; ++c) {
-              const u32x4 x = *reinterpret_cast<const u32x4*>(buf + TL::k_offset(row_lane, c));
+          for (int c = 0; c < S::DC / 2; ++c) {
+            const int cc = c0 + c;
+            const u32x4 x = *reinterpret_cast<const u32x4*>(buf + TL::k_offset(r, cc));
 #pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                const uint32_t w = x[e >> 1];
-                proxy = fmaf(s_qm[wave][8 * c + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)), proxy);
-              }
+            for (int e = 0; e < 8; ++e) {
+              const uint32_t w = x[e >> 1];
+              part[e & 3] = fmaf(s_qm[qg][8 * cc + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)),
+                                 part[e & 3]);
             }
-            sel = proxy > s_cut[wave];
-            if (p.dbg_proxy) p.dbg_proxy[row + j] = proxy * p.scale;
           }
-          sel = sel || (p.local_blocks >= 0 && abs(j - qbg) <= p.local_blocks) ||
-                j < p.kv_sink_blocks || qbg < p.q_sink_blocks;
-          if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qbg) * nkb + j] != 0;
-          if (p.dbg_selected) p.dbg_selected[row + j] = sel ? 1 : 0;
+          const float proxy = pair_sum((part[0] + part[1]) + (part[2] + part[3]));
+          sel = proxy > s_cut[qg];
+          if (p.dbg_proxy && hh == 0) p.dbg_proxy[dbg_row + j] = proxy * p.scale;
         }
-        const uint64_t bal = __ballot(sel);
-        if (lane == 0) {
-          s_mask[wave][2 * ct] = uint32_t(bal);
-          s_mask[wave][2 * ct + 1] = uint32_t(bal >> 32);
-        }
+        sel = sel || (p.local_blocks >= 0 && abs(j - qb) <= p.local_blocks) || j < p.kv_sink_blocks ||
+              qb < p.q_sink_blocks;
+        if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * nkb + j] != 0;
+        if (p.dbg_selected && hh == 0) p.dbg_selected[dbg_row + j] = sel ? 1 : 0;
       }
-      lds_barrier();
+      const uint64_t bal = __ballot(sel);
+      if (lane == 0) s_mask[qg][2 * ct + qh] = uint32_t(bal);
+      TileFrags<D> f;
+      if (live) {
+        tile_scores<D, 2>(buf, 0, qf, col, hh, f.p, f.va, refill);
+      } else {
+        refill.all();
+      }
+      lds_barrier();  // publishes the mask words for compute
+      return f;
+    };
+    auto compute = [&](TileFrags<D>& f, int ct) {
       if (live) {
         const uint64_t approx = tile_approx(s_mask[qg], ct, nkb);
-        if (approx) centroid_block<D>(buf, ct, approx, tk, scale_log2, qf, col, hh, st);
+        if (approx) centroid_finish<D>(f, ct, approx, tk, scale_log2, hh, st);
       }
     };
     tile_stream<D, NT, R>(ring, p.NCT, RangeCursor{0},
-                          [&](int ct) { return ctiles + int64_t(ct) * S::TILE; }, process, wave, lane);
+                          [&](int ct) { return ctiles + int64_t(ct) * S::TILE; }, load, compute, wave,
+                          lane);
     lds_barrier();  // every wave is done with the ring's centroid tiles
   }
   if (live && p.counts && lt == 0) {
@@ -588,8 +651,17 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
   const uint16_t* tiles = p.tiles + head * nkb * S::TILE;
   tile_stream<D, NT, R>(
       ring, count, cursor, [&](int j) { return tiles + int64_t(j) * S::TILE; },
-      [&](const uint16_t* buf, int j) {
-        if ((my_mask[j >> 5] >> (j & 31)) & 1u) exact_block<D>(buf, j, tk, scale_log2, qf, col, hh, st);
+      [&](const uint16_t* buf, int j, const TileRefill<D, NT>& refill) {
+        TileFrags<D> f;
+        if ((my_mask[j >> 5] >> (j & 31)) & 1u) {
+          tile_scores<D, 2>(buf, 0, qf, col, hh, f.p, f.va, refill);
+        } else {
+          refill.all();
+        }
+        return f;
+      },
+      [&](TileFrags<D>& f, int j) {
+        if ((my_mask[j >> 5] >> (j & 31)) & 1u) exact_finish<D>(f, j, tk, scale_log2, hh, st);
       },
       wave, lane);
 
@@ -639,8 +711,12 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
   tile_stream<D, NT, 2>(
       ring, p.NKB, RangeCursor{0}, [&](int j) { return tiles + int64_t(j) * S::TILE; },
-      [&](const uint16_t* buf, int j) { exact_block<D>(buf, j, tk, scale_log2, qf, col, hh, st); },
-      wave, lane);
+      [&](const uint16_t* buf, int, const TileRefill<D, NT>& refill) {
+        TileFrags<D> f;
+        tile_scores<D, 2>(buf, 0, qf, col, hh, f.p, f.va, refill);
+        return f;
+      },
+      [&](TileFrags<D>& f, int j) { exact_finish<D>(f, j, tk, scale_log2, hh, st); }, wave, lane);
   store_output<D>(p, b, h, q0 + myq, hh, st);
 }
 
