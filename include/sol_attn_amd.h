@@ -13,6 +13,12 @@
  *    pointer ([batch, tokens] int64, device memory) is given, token t of
  *    batch b is row index[b * tokens + t] and the batch stride is ignored
  *    (indexed windows, indexed.py:99).
+ *  - Ragged indexed windows: key_lengths (int32 [batch], device memory; NULL =
+ *    every entry has key_tokens keys) gives entry b's key count, 1..key_tokens;
+ *    its keys are the first key_lengths[b] rows of its key_index row, and every
+ *    buffer keeps the key_tokens-sized layout (out-of-range values are clamped
+ *    into 1..key_tokens).  The reference supports equal-length windows only;
+ *    this runs windows of different key counts in one call.
  *  - Row starts must be 16-byte aligned: base pointers 16-byte aligned and
  *    strides multiples of 8 elements.
  *  - The library never allocates or frees device memory.  Launches are
@@ -31,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 1
+#define SOL_ABI_VERSION 2
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
 
@@ -69,7 +75,7 @@ int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t hea
  * variance of the BF16 key centroids. */
 int sol_pool_kv(const void* k, const int64_t* k_strides,
                 const void* v, const int64_t* v_strides,
-                const int64_t* key_index,
+                const int64_t* key_index, const int32_t* key_lengths,
                 int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
                 void* ctiles, void* tiles,
                 float* chunk_sums, float* key_mean, float* key_var,
@@ -82,20 +88,24 @@ int sol_pool_kv(const void* k, const int64_t* k_strides,
  * only); key_mean/key_var are read only for finite beta.  local_blocks < 0
  * disables the local band (indexed windows).  Sink token counts round
  * outward to whole blocks.  protection: NULL or uint8 [batch, NQB, NKB].
- * out: contiguous BF16 [batch, query_tokens, heads, head_dim].
+ * out: contiguous BF16 [batch, query_tokens, heads, head_dim]; or, when
+ * out_index (int64 [batch, query_tokens], device) is given, a contiguous BF16
+ * [N, heads, head_dim] whose row out_index[b * query_tokens + t] receives
+ * query t of entry b (the scatter `out[rows] = result` of a window adapter,
+ * integrations/vdn.py:67-74, fused into the store; rows must be distinct).
  * counts: NULL or int32 [batch, NQB, heads] exact-block counts.
  * debug_selected (uint8) / debug_proxy (fp32): NULL or [batch, NQB, heads, NKB]
  * routing decisions and proxies (natural-log units); debug_cutoff: NULL or
  * fp32 [batch, NQB, heads].  Debug outputs are for verification, not timing. */
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t batch, int64_t query_tokens, int64_t key_tokens,
-                      int64_t heads, int64_t head_dim,
+                      const int32_t* key_lengths, int64_t heads, int64_t head_dim,
                       const void* tiles, const void* ctiles,
                       const float* key_mean, const float* key_var,
                       const uint8_t* protection,
                       double scale, double beta, int64_t local_blocks,
                       int64_t kv_sink_tokens, int64_t query_sink_tokens,
-                      void* out, int32_t* counts,
+                      void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
                       void* stream);
 

@@ -17,7 +17,7 @@ import torch
 
 BLOCK = 64
 MAX_KEY_BLOCKS = 8192
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -32,12 +32,12 @@ _SIGNATURES = {
     "sol_abi_version": ([], ctypes.c_int),
     "sol_last_error": ([], ctypes.c_char_p),
     "sol_pool_sizes": ([_i64, _i64, _i64, _i64, _i64p], ctypes.c_int),
-    "sol_pool_kv": ([_p, _i64p, _p, _i64p, _p, _i64, _i64, _i64, _i64,
+    "sol_pool_kv": ([_p, _i64p, _p, _i64p, _p, _p, _i64, _i64, _i64, _i64,
                      _p, _p, _p, _p, _p, _p], ctypes.c_int),
-    "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _i64,
+    "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _p, _i64, _i64,
                            _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
-                           _p, _p, _p, _p, _p, _p], ctypes.c_int),
+                           _p, _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
                        _dbl, _p, _p, _p], ctypes.c_int),
 }
@@ -95,13 +95,15 @@ def _tiles(b, h, nkb, d, device):
     return torch.empty((b, h, nkb, 2, BLOCK * d), device=device, dtype=torch.bfloat16)
 
 
-def pool_kv(k, v, key_index=None, moments=True):
+def pool_kv(k, v, key_index=None, moments=True, key_lengths=None):
     """Centroid tiles, attention tiles and key moments (one HBM pass over K and V).
 
     ``k``/``v``: ``[B, Tk, H, D]`` BF16 or, with ``key_index`` ``[B, Tk]``,
-    NHD ``[N, H, D]``.  Returns a dict with ``ctiles`` ``[B, H, NCT, 2, 64 D]``
-    (block centroids), ``tiles`` ``[B, H, NKB, 2, 64 D]`` and ``mean``/``var``
-    ``[B, H, D]`` (None without ``moments``); layouts per ``include/sol_attn_amd.h``.
+    NHD ``[N, H, D]``.  ``key_lengths`` (int32 ``[B]`` on the device, ragged
+    windows): entry b uses its first ``key_lengths[b]`` keys.  Returns a dict
+    with ``ctiles`` ``[B, H, NCT, 2, 64 D]`` (block centroids), ``tiles``
+    ``[B, H, NKB, 2, 64 D]`` and ``mean``/``var`` ``[B, H, D]`` (None without
+    ``moments``); layouts per ``include/sol_attn_amd.h``.
     """
     lib = library()
     indexed = key_index is not None
@@ -122,19 +124,21 @@ def pool_kv(k, v, key_index=None, moments=True):
         mean = torch.empty((b, h, d), device=dev, dtype=torch.float32)
         var = torch.empty_like(mean)
     _check(lib.sol_pool_kv(_ptr(k), _strides(k, indexed), _ptr(v), _strides(v, indexed),
-                           _ptr(key_index), b, tk, h, d, _ptr(ctiles), _ptr(tiles),
-                           _ptr(sums), _ptr(mean), _ptr(var), _stream(dev)))
+                           _ptr(key_index), _ptr(key_lengths), b, tk, h, d, _ptr(ctiles),
+                           _ptr(tiles), _ptr(sums), _ptr(mean), _ptr(var), _stream(dev)))
     return {"ctiles": ctiles, "tiles": tiles, "mean": mean, "var": var, "key_tokens": tk,
-            "key_blocks": nkb}
+            "key_blocks": nkb, "key_lengths": key_lengths}
 
 
 def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows=None,
-           debug=False):
+           debug=False, out=None):
     """Routing + attention over pooled keys (the ``_sol`` launch of ``kernels.py:218-224``).
 
     ``pooled`` is the dict returned by :func:`pool_kv`.  ``rows`` (indexed
-    windows) gathers the query rows.  Returns ``(out, counts, dbg)``; ``dbg``
-    is None unless ``debug``.
+    windows) gathers the query rows.  With ``out`` (a contiguous BF16
+    ``[N, H, D]`` tensor, indexed windows only) query i of window w is stored
+    at ``out[rows[w, i]]`` instead of into a new ``[W, nq, H, D]`` tensor.
+    Returns ``(out, counts, dbg)``; ``dbg`` is None unless ``debug``.
     """
     lib = library()
     indexed = rows is not None
@@ -146,7 +150,14 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     q = _rows(q)
     dev = q.device
     nqb = -(-nq // BLOCK)
-    out = torch.empty((b, nq, h, d), device=dev, dtype=torch.bfloat16)
+    scatter = out is not None
+    if scatter:
+        if not indexed or out.dtype != torch.bfloat16 or not out.is_contiguous() \
+                or out.ndim != 3 or out.shape[1:] != (h, d) or out.device != dev:
+            raise ValueError("out must be a contiguous BF16 [N, H, D] tensor on the Q device "
+                             "(indexed windows only)")
+    else:
+        out = torch.empty((b, nq, h, d), device=dev, dtype=torch.bfloat16)
     counts = torch.empty((b, nqb, h), device=dev, dtype=torch.int32)
     dbg = None
     if debug:
@@ -157,11 +168,11 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     if protection is not None:
         prot = protection.contiguous().view(torch.uint8)
     _check(lib.sol_attention_fwd(
-        _ptr(q), _strides(q, indexed), _ptr(rows), b, nq, nk, h, d,
+        _ptr(q), _strides(q, indexed), _ptr(rows), b, nq, nk, _ptr(pooled.get("key_lengths")), h, d,
         _ptr(pooled["tiles"]), _ptr(pooled["ctiles"]),
         _ptr(pooled["mean"]), _ptr(pooled["var"]),
         _ptr(prot), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
-        _ptr(out), _ptr(counts),
+        _ptr(out), _ptr(rows if scatter else None), _ptr(counts),
         _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
         _stream(dev)))
     if debug:
@@ -170,16 +181,18 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
 
 
 def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=None,
-               rows=None, keys=None, debug=False):
+               rows=None, keys=None, debug=False, key_lengths=None, out=None):
     """All-in SOL attention (``kernels.py:203-225``): pooling, moments, routing, attention.
 
     ``rows``/``keys`` (indexed windows) gather Q and K/V token rows inside the
-    kernels instead of materialising copies.  Returns ``(out, counts)`` and,
-    with ``debug=True``, a dict of routing diagnostics as a third element.
+    kernels instead of materialising copies; ``key_lengths`` makes the windows'
+    key counts ragged and ``out`` scatters the result rows (see :func:`attend`).
+    Returns ``(out, counts)`` and, with ``debug=True``, a dict of routing
+    diagnostics as a third element.
     """
-    pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta))
+    pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths)
     out, counts, dbg = attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection, rows,
-                              debug)
+                              debug, out)
     if debug:
         dbg.update(pooled)
         return out, counts, dbg

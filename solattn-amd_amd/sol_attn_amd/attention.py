@@ -16,13 +16,18 @@ class SolStats:
     """Exact-block statistics (``attention.py:9-16``).
 
     ``exact_blocks`` is a device int32 tensor ``[batch, query_blocks, heads]``;
-    ``density()`` synchronises to produce a Python float.
+    ``density()`` synchronises to produce a Python float.  ``key_blocks`` is
+    an int, or, for ragged indexed windows, a ``[batch]`` tensor of each
+    window's key blocks; density is then the mean of exact / key blocks.
     """
 
     exact_blocks: torch.Tensor
-    key_blocks: int
+    key_blocks: "int | torch.Tensor"
 
     def density(self) -> float:
+        if isinstance(self.key_blocks, torch.Tensor):
+            kb = self.key_blocks.to(self.exact_blocks.device, torch.float32).view(-1, 1, 1)
+            return (self.exact_blocks.float() / kb).mean().item()
         return self.exact_blocks.float().mean().item() / self.key_blocks
 
 

@@ -351,7 +351,8 @@ __device__ __forceinline__ void store_output(const AttnParams& p, int b, int h, 
   using S = Shape<D>;
   const float den = pair_sum(st.den);
   if (t >= p.Tq) return;
-  uint16_t* orow = p.out + ((int64_t(b) * p.Tq + t) * p.H + h) * D;
+  const int64_t row = p.out_index ? p.out_index[int64_t(b) * p.Tq + t] : int64_t(b) * p.Tq + t;
+  uint16_t* orow = p.out + (row * p.H + h) * D;
 #pragma unroll
   for (int dt = 0; dt < S::DT; ++dt)
 #pragma unroll
@@ -507,7 +508,9 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
   const int qb0 = task.tile * G;
   const int qb = qb0 + qg;
   const bool live = qb < p.NQB;
-  const int nkb = p.NKB, tk = p.Tk;
+  const int tk = batch_tokens(p.klen, b, p.Tk);  // this entry's key tokens
+  const int nkb = (tk + kBlock - 1) / kBlock;      // its key blocks (<= p.NKB, the buffer stride)
+  const int nct = (nkb + kBlock - 1) / kBlock;     // its centroid tiles (<= p.NCT)
   const float scale_log2 = p.scale_log2;
 
   // 1. Q tiles -> LDS -> fragments.
@@ -562,7 +565,7 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
     if (tid < G) s_cut[tid] = (s_red[tid][0] + s_red[tid][1]) + p.beta * sqrtf(s_red[tid][2] + s_red[tid][3]);
   }
   __syncthreads();  // cutoffs published; Q staging is dead and the ring is free
-  const int64_t dbg_row = ((int64_t(b) * p.NQB + qb) * p.H + h) * nkb;
+  const int64_t dbg_row = ((int64_t(b) * p.NQB + qb) * p.H + h) * p.NKB;
   if (live && p.dbg_cutoff && lt == 0)
     p.dbg_cutoff[(int64_t(b) * p.NQB + qb) * p.H + h] =
         p.force == 0 ? s_cut[qg] * p.scale : (p.force == 1 ? kNegInf : -kNegInf);
@@ -613,7 +616,7 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
         }
         sel = sel || (p.local_blocks >= 0 && abs(j - qb) <= p.local_blocks) || j < p.kv_sink_blocks ||
               qb < p.q_sink_blocks;
-        if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * nkb + j] != 0;
+        if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * p.NKB + j] != 0;
         if (p.dbg_selected && hh == 0) p.dbg_selected[dbg_row + j] = sel ? 1 : 0;
       }
       const uint64_t bal = __ballot(sel);
@@ -633,7 +636,7 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
         if (approx) centroid_finish<D>(f, ct, approx, tk, scale_log2, hh, st);
       }
     };
-    tile_stream<D, NT, R>(ring, p.NCT, RangeCursor{0},
+    tile_stream<D, NT, R>(ring, nct, RangeCursor{0},
                           [&](int ct) { return ctiles + int64_t(ct) * S::TILE; }, load, compute, wave,
                           lane);
     lds_barrier();  // every wave is done with the ring's centroid tiles
@@ -648,7 +651,7 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
   UnionCursor<G> cursor{&s_mask[0][0], kMaskWords, nkb};
   const int count = cursor.count();
   const uint32_t* my_mask = s_mask[qg];
-  const uint16_t* tiles = p.tiles + head * nkb * S::TILE;
+  const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
   tile_stream<D, NT, R>(
       ring, count, cursor, [&](int j) { return tiles + int64_t(j) * S::TILE; },
       [&](const uint16_t* buf, int j, const TileRefill<D, NT>& refill) {

@@ -77,7 +77,8 @@ int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t hea
 namespace {
 
 int pool_checked(const char* who, const void* k, const int64_t* k_strides, const void* v,
-                 const int64_t* v_strides, const int64_t* key_index, int64_t batch,
+                 const int64_t* v_strides, const int64_t* key_index, const int32_t* key_lengths,
+                 int64_t batch,
                  int64_t key_tokens, int64_t heads, int64_t head_dim, void* ctiles, void* tiles,
                  float* chunk_sums, float* key_mean, float* key_var, void* stream) {
   static thread_local std::string msg;
@@ -101,6 +102,7 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
   sol::PoolParams p;
   p.k = rows_of(k, k_strides, key_index, key_tokens);
   p.v = rows_of(v, v_strides, key_index, key_tokens);
+  p.klen = key_lengths;
   p.ctiles = static_cast<uint16_t*>(ctiles);
   p.tiles = static_cast<uint16_t*>(tiles);
   p.ksum = moments ? chunk_sums : nullptr;
@@ -118,19 +120,21 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
 }  // namespace
 
 int sol_pool_kv(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
-                const int64_t* key_index, int64_t batch, int64_t key_tokens, int64_t heads,
-                int64_t head_dim, void* ctiles, void* tiles, float* chunk_sums, float* key_mean,
-                float* key_var, void* stream) {
-  return pool_checked("sol_pool_kv", k, k_strides, v, v_strides, key_index, batch, key_tokens,
-                      heads, head_dim, ctiles, tiles, chunk_sums, key_mean, key_var, stream);
+                const int64_t* key_index, const int32_t* key_lengths, int64_t batch,
+                int64_t key_tokens, int64_t heads, int64_t head_dim, void* ctiles, void* tiles,
+                float* chunk_sums, float* key_mean, float* key_var, void* stream) {
+  return pool_checked("sol_pool_kv", k, k_strides, v, v_strides, key_index, key_lengths, batch,
+                      key_tokens, heads, head_dim, ctiles, tiles, chunk_sums, key_mean, key_var,
+                      stream);
 }
 
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
-                      int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
-                      int64_t head_dim, const void* tiles, const void* ctiles,
-                      const float* key_mean, const float* key_var, const uint8_t* protection,
-                      double scale, double beta, int64_t local_blocks, int64_t kv_sink_tokens,
-                      int64_t query_sink_tokens, void* out, int32_t* counts,
+                      int64_t batch, int64_t query_tokens, int64_t key_tokens,
+                      const int32_t* key_lengths, int64_t heads, int64_t head_dim,
+                      const void* tiles, const void* ctiles, const float* key_mean,
+                      const float* key_var, const uint8_t* protection, double scale, double beta,
+                      int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens,
+                      void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
                       void* stream) {
   if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
@@ -157,6 +161,8 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   sol::AttnParams p;
   std::memset(&p, 0, sizeof(p));
   p.q = rows_of(q, q_strides, query_index, query_tokens);
+  p.klen = key_lengths;
+  p.out_index = out_index;
   p.tiles = static_cast<const uint16_t*>(tiles);
   p.ctiles = static_cast<const uint16_t*>(ctiles);
   p.mean = key_mean;
@@ -199,7 +205,7 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
   if (!out || !aligned16(out)) return fail(SOL_ERR_INVALID, "sol_dense_fwd: out must be 16-byte aligned");
   if (batch * heads * cdiv(query_tokens, 128) >= (int64_t(1) << 31))
     return fail(SOL_ERR_UNSUPPORTED, "sol_dense_fwd: grid too large");
-  const int rc = pool_checked("sol_dense_fwd", k, k_strides, v, v_strides, nullptr, batch,
+  const int rc = pool_checked("sol_dense_fwd", k, k_strides, v, v_strides, nullptr, nullptr, batch,
                               key_tokens, heads, head_dim, nullptr, tiles, nullptr, nullptr,
                               nullptr, stream);
   if (rc != SOL_OK) return rc;

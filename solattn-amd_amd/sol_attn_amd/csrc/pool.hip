@@ -36,6 +36,8 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
   const int h = bh % p.H, b = bh / p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int sub = lane / LPB, r4 = (lane % LPB) / DC, dc = lane % DC;
+  const int tk = batch_tokens(p.klen, b, p.Tk);  // this entry's key tokens
+  const int nkb = (tk + kBlock - 1) / kBlock;
 
 #pragma unroll
   for (int it = 0; it < 4 / BPI; ++it) {
@@ -45,8 +47,8 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) s[e] = 0.f;
     int len = 0;
-    if (j < p.NKB) {
-      len = min(kBlock, p.Tk - kBlock * j);
+    if (j < nkb) {
+      len = min(kBlock, tk - kBlock * j);
       u32x4 x[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
@@ -129,9 +131,9 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
           *reinterpret_cast<const u32x4*>(&cent[jb][8 * cc]);
     }
     // Chunk partial sums of the BF16 centroids and their squares (moments).
-    const int nch = (p.NKB + kPoolChunk - 1) / kPoolChunk;
-    if (p.ksum && c < nch && tid < D) {
-      const int rows = min(kPoolChunk, p.NKB - c * kPoolChunk);
+    const int nch = (p.NKB + kPoolChunk - 1) / kPoolChunk;  // layout stride
+    if (p.ksum && c * kPoolChunk < nkb && tid < D) {
+      const int rows = min(kPoolChunk, nkb - c * kPoolChunk);
       float s1 = 0.f, s2 = 0.f;
       for (int jb = 0; jb < rows; ++jb) {
         const float x = bf16_bits_to_f32(cent[jb][tid]);
@@ -162,11 +164,14 @@ constexpr int kGroupsPerPass = 32;
 template <int D>
 __global__ __launch_bounds__(kMomentThreads) void moments_kernel(const float* __restrict__ ksum,
                                                                  float* __restrict__ mean,
-                                                                 float* __restrict__ var, int nkb) {
+                                                                 float* __restrict__ var,
+                                                                 const int32_t* __restrict__ klen,
+                                                                 int tk_all, int nkb_all, int heads) {
   constexpr int G = kMomentThreads / D;  // threads per feature
   __shared__ float gs[2][kGroupsPerPass][D];
   const int bh = blockIdx.x, d = threadIdx.x % D, gi = threadIdx.x / D;
-  const int nch = (nkb + kPoolChunk - 1) / kPoolChunk;
+  const int nkb = (batch_tokens(klen, bh / heads, tk_all) + kBlock - 1) / kBlock;  // this entry's blocks
+  const int nch = (nkb_all + kPoolChunk - 1) / kPoolChunk;  // layout stride of the chunk sums
   const int full_chunks = nkb / kPoolChunk;
   const int full_groups = full_chunks / 16;
   const float* base = ksum + int64_t(bh) * nch * 2 * D;
@@ -207,7 +212,7 @@ __global__ __launch_bounds__(kMomentThreads) void moments_kernel(const float* __
     a1[0] = a1[0] + base[(2 * c) * D + d];
     a1[1] = a1[1] + base[(2 * c + 1) * D + d];
   }
-  if (full_chunks < nch) {
+  if (full_chunks * kPoolChunk < nkb) {
     rem[0] = base[(2 * full_chunks) * D + d];
     rem[1] = base[(2 * full_chunks + 1) * D + d];
   }
@@ -229,10 +234,10 @@ hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
   if (err != hipSuccess || !p.ksum || !p.ctiles) return err;
   if (D == 128)
     hipLaunchKernelGGL(moments_kernel<128>, dim3(p.B * p.H), dim3(kMomentThreads), 0, stream,
-                       p.ksum, p.mean, p.var, p.NKB);
+                       p.ksum, p.mean, p.var, p.klen, p.Tk, p.NKB, p.H);
   else
     hipLaunchKernelGGL(moments_kernel<64>, dim3(p.B * p.H), dim3(kMomentThreads), 0, stream,
-                       p.ksum, p.mean, p.var, p.NKB);
+                       p.ksum, p.mean, p.var, p.klen, p.Tk, p.NKB, p.H);
   return hipGetLastError();
 }
 

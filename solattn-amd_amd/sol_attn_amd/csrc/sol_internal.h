@@ -8,29 +8,41 @@
 
 namespace sol {
 
+// Key tokens of batch entry b: klen[b] clamped to [1, T] when per-entry
+// lengths are given (ragged indexed windows), else T.  The clamp keeps every
+// access inside the [B, T]-shaped index and the NKB-padded buffers whatever
+// the caller's lengths hold.
+__device__ __forceinline__ int batch_tokens(const int32_t* klen, int b, int T) {
+  return klen ? min(max(klen[b], 1), T) : T;
+}
+
 struct PoolParams {
   TokenRows k, v;
+  const int32_t* klen;  // [B] key tokens per batch entry (<= Tk), or null: all Tk
   uint16_t* ctiles;  // [B, H, NCT, 2, 64 * D] centroid tiles, or null (tiles only)
   uint16_t* tiles;   // [B, H, NKB, 2, 64 * D] swizzled K / V^T block tiles, or null
   float* ksum;       // [B, H, NCH, 2, D] chunk sums, null -> no moments
   float* mean;       // [B, H, D]
   float* var;        // [B, H, D]
   int B, H, Tk, NKB, NCT, NCHP;  // NCHP = 4 * NCT pooling chunks of 16 blocks
+                                 // (NKB, NCT: for Tk; ragged entries use a prefix)
 };
 
 struct AttnParams {
   TokenRows q;
+  const int32_t* klen;         // [B] key tokens per batch entry (<= Tk), or null: all Tk
+  const int64_t* out_index;    // [B, Tq] output rows of an [N, H, D] output, or null
   const uint16_t* tiles;       // [B, H, NKB, 2, 64 * D] from the pooling pass
   const uint16_t* ctiles;      // [B, H, NCT, 2, 64 * D] centroid tiles
   const float* mean;           // [B, H, D]
   const float* var;            // [B, H, D]
   const uint8_t* protection;   // [B, NQB, NKB] or null
-  uint16_t* out;               // [B, Tq, H, D]
+  uint16_t* out;               // [B, Tq, H, D], or [N, H, D] rows out_index
   int32_t* counts;             // [B, NQB, H] or null
   uint8_t* dbg_selected;       // [B, NQB, H, NKB] or null
   float* dbg_proxy;            // [B, NQB, H, NKB] or null
   float* dbg_cutoff;           // [B, NQB, H] or null
-  int B, H, Tq, Tk, NQB, NKB, NCT;
+  int B, H, Tq, Tk, NQB, NKB, NCT;  // NKB, NCT: buffer strides for Tk
   float scale, scale_log2, beta;
   int force;          // 0 finite beta, 1 beta = -inf (all exact), 2 beta = +inf
   int local_blocks;   // < 0 disables the local band

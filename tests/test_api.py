@@ -127,7 +127,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == 1
+    assert native.sol_abi_version() == 2
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -145,14 +145,63 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     rc = native.sol_dense_fwd(fake, strides, fake, strides, fake, strides, 1, 193, 317, 2, 64,
                               float("nan"), fake, fake, None)
     assert rc == -1 and b"scale" in native.sol_last_error()
-    rc = native.sol_attention_fwd(fake, strides, None, 1, 193, 317, 2, 64, fake, fake,
+    rc = native.sol_attention_fwd(fake, strides, None, 1, 193, 317, None, 2, 64, fake, fake,
                                   None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None,
-                                  None, None)
+                                  None, None, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
     bad = (ctypes.c_int64 * 3)(64 * 2 * 317, 127, 64)
-    rc = native.sol_pool_kv(fake, bad, fake, strides, None, 1, 317, 2, 64, fake, fake,
+    rc = native.sol_pool_kv(fake, bad, fake, strides, None, None, 1, 317, 2, 64, fake, fake,
                             None, None, None, None)
     assert rc == -1 and b"aligned" in native.sol_last_error()
-    rc = native.sol_pool_kv(fake, strides, fake, strides, None, 1, 317, 2, 64, None, None,
+    rc = native.sol_pool_kv(fake, strides, fake, strides, None, None, 1, 317, 2, 64, None, None,
                             None, None, None, None)
     assert rc == -1 and b"nothing to write" in native.sol_last_error()
+
+
+def test_ragged_plan_matches_oracle_per_window():
+    from oracle.sol_oracle import plan_protection
+    rng = np.random.default_rng(21)
+    for trial in range(12):
+        w, seq = int(rng.integers(2, 5)), int(rng.integers(400, 3000))
+        nq = int(rng.integers(1, 200))
+        rows = np.stack([np.sort(rng.choice(seq, nq, replace=False)) for _ in range(w)])
+        keys = [np.sort(rng.choice(seq, int(rng.integers(1, 400)), replace=False)) for _ in range(w)]
+        a = int(rng.integers(0, seq - 1))
+        ranges = ((a, int(rng.integers(a + 1, seq + 1))),)
+        local = int(rng.integers(0, 100))
+        p = IndexedPlan.create(torch.from_numpy(rows), [torch.from_numpy(x) for x in keys], seq,
+                               protected_ranges=ranges, local_tokens=local)
+        nk = max(len(x) for x in keys)
+        assert p.keys.shape == (w, nk) and p.key_lengths.tolist() == [len(x) for x in keys]
+        assert p.protected_blocks.shape == (w, -(-nq // 64), -(-nk // 64))
+        for i, x in enumerate(keys):
+            nkb = -(-len(x) // 64)
+            np.testing.assert_array_equal(p.keys[i, :len(x)].numpy(), x)
+            expect = plan_protection(rows[i:i + 1], x[None], seq, ranges, local)[0]
+            np.testing.assert_array_equal(p.protected_blocks[i, :, :nkb].numpy(), expect)
+            assert not p.protected_blocks[i, :, nkb:].any()
+        # An equal-length plan built from the same window agrees.
+        q = IndexedPlan.create(torch.from_numpy(rows[:1]), torch.from_numpy(keys[0][None]), seq,
+                               protected_ranges=ranges, local_tokens=local)
+        assert q.key_lengths is None
+        np.testing.assert_array_equal(q.protected_blocks[0].numpy(),
+                                      p.protected_blocks[0, :, :q.protected_blocks.shape[2]].numpy())
+
+
+@pytest.mark.parametrize("kind", ["empty", "unsorted", "outside", "count", "matrix", "dtype"])
+def test_ragged_plan_rejects_invalid_keys(kind):
+    rows = torch.tensor([[1, 2], [5, 6]], dtype=torch.int64)
+    keys = [torch.arange(8), torch.arange(3, 12)]
+    if kind == "empty": keys[1] = keys[1][:0]
+    if kind == "unsorted": keys[0] = keys[0].flip(0)
+    if kind == "outside": keys[1] = torch.arange(15, 25)
+    if kind == "count": keys = keys[:1]
+    if kind == "matrix": keys[0] = keys[0].reshape(2, 4)
+    if kind == "dtype": keys[1] = keys[1].int()
+    with pytest.raises(ValueError):
+        IndexedPlan.create(rows, keys, 20)
+
+
+def test_stats_density_ragged_windows():
+    exact = torch.tensor([[[2], [4]], [[1], [1]]], dtype=torch.int32)
+    assert SolStats(exact, torch.tensor([4, 2])).density() == pytest.approx((0.5 + 1 + 0.5 + 0.5) / 4)

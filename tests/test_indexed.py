@@ -61,3 +61,54 @@ def test_indexed_equals_bthd_on_gathered_rows():
                                 local_blocks=-1, protected_blocks=p.protected_blocks.cpu())
     np.testing.assert_array_equal(stats.exact_blocks.cpu().numpy(), counts)
     torch.testing.assert_close(out.cpu().float(), torch.from_numpy(ref), atol=0.012, rtol=0.025)
+
+
+def _ragged_case(seed, n=1500, heads=2, d=128):
+    g = torch.Generator().manual_seed(seed)
+    x = [torch.randn((n, heads, d), generator=g, dtype=torch.bfloat16) for _ in range(3)]
+    rows = torch.stack((torch.arange(64, 194), torch.arange(500, 630), torch.arange(1300, 1430)))
+    keys = [torch.cat((torch.arange(0, 7), torch.arange(40, 300))),     # 267 keys, 5 blocks
+            torch.cat((torch.arange(0, 7), torch.arange(380, 1000))),   # 627 keys, 10 blocks
+            torch.arange(1250, 1330)]                                  # 80 keys, 2 blocks
+    return x, rows, keys
+
+
+@pytest.mark.parametrize("beta", [-math.inf, math.inf, 1.0, 0.0])
+def test_ragged_windows_one_call_equal_separate_calls_and_oracle(beta):
+    x, rows, keys = _ragged_case(11)
+    kw = dict(protected_ranges=((0, 7),), local_tokens=64)
+    p = IndexedPlan.create(rows, keys, 1500, **kw)
+    gpu = [t.cuda() for t in x]
+    out, stats = sol_attention_indexed(*gpu, p.to("cuda"), beta=beta, return_stats=True)
+    assert out.shape == (3, 130, 2, 128)
+    densities = []
+    for w in range(3):
+        pw = IndexedPlan.create(rows[w:w + 1], keys[w][None], 1500, **kw)
+        ow, sw = sol_attention_indexed(*gpu, pw.to("cuda"), beta=beta, return_stats=True)
+        assert torch.equal(out[w:w + 1], ow), f"window {w} differs from its own call"
+        assert torch.equal(stats.exact_blocks[w:w + 1], sw.exact_blocks)
+        ref, counts, _ = sol_oracle(x[0][rows[w:w + 1]], x[1][keys[w][None]], x[2][keys[w][None]],
+                                    beta=beta, local_blocks=-1, protected_blocks=pw.protected_blocks)
+        got = out[w:w + 1].cpu().float()
+        torch.testing.assert_close(got, torch.from_numpy(ref), atol=0.012, rtol=0.025)
+        assert (got - torch.from_numpy(ref)).norm() / np.linalg.norm(ref) < 0.008
+        np.testing.assert_array_equal(stats.exact_blocks[w:w + 1].cpu().numpy(), counts)
+        densities.append(counts.mean() / -(-len(keys[w]) // 64))
+    assert stats.density() == pytest.approx(float(np.mean(densities)), rel=1e-6)
+
+
+def test_scatter_epilogue_equals_indexed_assignment():
+    x, rows, keys = _ragged_case(12)
+    gpu = [t.cuda() for t in x]
+    for plan in (IndexedPlan.create(rows, keys, 1500),
+                 IndexedPlan.create(rows, torch.stack([k[:80] for k in keys]), 1500)):
+        p = plan.to("cuda")
+        ref = sol_attention_indexed(*gpu, p, beta=1.0)
+        out = torch.full_like(gpu[0], 3.0)
+        got = sol_attention_indexed(*gpu, p, beta=1.0, out=out)
+        assert got is out
+        expected = torch.full_like(gpu[0], 3.0)
+        expected[p.rows] = ref
+        assert torch.equal(out, expected)
+    with pytest.raises(ValueError, match="out must be"):
+        sol_attention_indexed(*gpu, p, out=torch.empty_like(gpu[0]).float())
