@@ -99,6 +99,85 @@ def routing_flops(selected, tq, tk, d):
     return exact, approx
 
 
+def window_plans(frames, tokens_per_frame):
+    """Video-DiT frame windows over the NHD sequence: window f's queries are
+    frame f, its keys frames {0, f-1, f, f+1}.  Returns (rows [W, nq],
+    per-window key vectors)."""
+    rows, keys = [], []
+    for f in range(frames):
+        fr = sorted({0, f - 1, f, f + 1} & set(range(frames)))
+        rows.append(torch.arange(f * tokens_per_frame, (f + 1) * tokens_per_frame))
+        keys.append(torch.cat([torch.arange(x * tokens_per_frame, (x + 1) * tokens_per_frame) for x in fr]))
+    return torch.stack(rows), keys
+
+
+def bench_windows(q, k, v, cfg, reps, check_cpu):
+    """Indexed windows on the same field viewed as NHD [N, H, D]: one ragged
+    call with the fused scatter vs the reference's route (one equal-length
+    plan per key count, results scattered with out[rows] = result)."""
+    from sol_attn_amd import IndexedPlan, sol_attention_indexed
+    qn, kn, vn = q[0], k[0], v[0]
+    n, h, d = qn.shape
+    tpf = cfg["height"] * cfg["width"]
+    rows, keys = window_plans(cfg["frames"], tpf)
+    prot = dict(protected_ranges=((0, tpf),), local_tokens=64)
+    t0 = time.perf_counter()
+    plan = IndexedPlan.create(rows, keys, n, **prot)
+    t_create = time.perf_counter() - t0
+    plan_dev = plan.to(q.device)
+    torch.cuda.synchronize()
+    t_setup = time.perf_counter() - t0
+    groups = {}
+    for w, kv in enumerate(keys):
+        groups.setdefault(len(kv), []).append(w)
+    eq_plans = [IndexedPlan.create(rows[ws], torch.stack([keys[w] for w in ws]), n, **prot).to(q.device)
+                for ws in groups.values()]
+    out = torch.empty_like(qn)
+
+    def ragged():
+        return sol_attention_indexed(qn, kn, vn, plan_dev, beta=cfg["beta"], out=out)
+
+    def per_length():
+        o = torch.empty_like(qn)
+        for p in eq_plans:
+            o[p.rows] = sol_attention_indexed(qn, kn, vn, p, beta=cfg["beta"])
+        return o
+
+    ragged(); per_length()
+    torch.cuda.synchronize()
+    ragged_ms = event_ms(ragged, reps)
+    per_ms = event_ms(per_length, reps)
+    _, stats = sol_attention_indexed(qn, kn, vn, plan_dev, beta=cfg["beta"], return_stats=True)
+    agree = bool(torch.equal(ragged(), per_length()))
+    flops = sum(4.0 * rows.shape[1] * len(kv) * h * d for kv in keys)
+    res = {"workload": f"{cfg['frames']} frame windows x {tpf} queries, keys = frames "
+                       "{0, f-1, f, f+1} (ragged: " + "/".join(str(x) for x in sorted(groups)) + ")",
+           "ragged_scatter_ms": ragged_ms, "per_key_count_plans_ms": per_ms,
+           "plans": len(groups), "speedup_one_call": per_ms / ragged_ms,
+           "dense_equiv_tflops": flops / (ragged_ms * 1e-3) / 1e12, "dense_equiv_flops": flops,
+           "density": stats.density(), "identical_to_per_plan_route": agree,
+           "plan_create_s": t_create, "plan_setup_s": t_setup}
+    if check_cpu:
+        from oracle import sol_oracle as orc
+        w = cfg["frames"] // 2
+        sample = [0, (rows.shape[1] // 64) // 2, (rows.shape[1] + 63) // 64 - 1]
+        kv = keys[w]
+        ref, counts, _ = orc.sol_oracle(qn[rows[w]].cpu().float().numpy()[None],
+                                        kn[kv].cpu().float().numpy()[None],
+                                        vn[kv].cpu().float().numpy()[None], beta=cfg["beta"],
+                                        local_blocks=-1, query_blocks=sample,
+                                        protected_blocks=plan.protected_blocks[w:w + 1, :, :-(-len(kv) // 64)].numpy())
+        rr = np.concatenate([np.arange(64 * x, min(rows.shape[1], 64 * x + 64)) for x in sample])
+        got = out[rows[w][rr]].float().cpu().numpy()
+        exp = ref[0, rr]
+        res["parity_vs_oracle"] = {"window": w, "sampled_query_blocks": sample,
+                                   "max_abs": float(np.abs(got - exp).max()),
+                                   "rel_l2": float(np.linalg.norm(got - exp) / np.linalg.norm(exp)),
+                                   "counts_equal": bool(np.array_equal(
+                                       stats.exact_blocks[w, sample].cpu().numpy(), counts[0, sample]))}
+    return res
+
+
 def measured_traffic(workload):
     """Memory-side bytes per launch of the SOL kernel, from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary of this workload (None if there is none)."""
@@ -162,6 +241,8 @@ def main():
     ap.add_argument("--cpu-blocks", type=int, default=24,
                     help="query blocks (evenly spaced, all heads) in the CPU oracle sample")
     ap.add_argument("--dense-reps", type=int, default=2)
+    ap.add_argument("--no-windows", action="store_true",
+                    help="skip the indexed frame-window measurement on the same field")
     ap.add_argument("--copy-gib", type=float, default=0.0,
                     help="also run a device copy of this many GiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -254,6 +335,8 @@ def main():
         "pool_roofline": {"bound": "hbm", "achieved": pool_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": pool_gbs / PEAK_HBM_GBS, "bytes_per_launch": pool_bytes},
     }
+    if "frames" in cfg and not args.no_windows:
+        result["indexed_windows"] = bench_windows(q, k, v, cfg, max(3, args.steps // 2), not args.no_cpu)
     if not args.no_cpu:
         nqb = (t + 63) // 64
         sample = sorted(set(np.linspace(0, nqb - 1, max(1, min(args.cpu_blocks, nqb))).round().astype(int).tolist()))

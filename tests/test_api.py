@@ -205,3 +205,28 @@ def test_ragged_plan_rejects_invalid_keys(kind):
 def test_stats_density_ragged_windows():
     exact = torch.tensor([[[2], [4]], [[1], [1]]], dtype=torch.int32)
     assert SolStats(exact, torch.tensor([4, 2])).density() == pytest.approx((0.5 + 1 + 0.5 + 0.5) / 4)
+
+
+def test_frame_window_plan_protection_floor():
+    # 21 frame windows of 4,032 (= 63 x 64) queries, keys = frames
+    # {0, f-1, f, f+1}, frame 0 protected, local 64.  Frame 0 fills key blocks
+    # 0..62 of every window: 63 x 63 = 3969 protected (q-block, key-block)
+    # pairs.  The local band of q-block qb touches token blocks qb-1, qb, qb+1
+    # of frame f (block -1 / 63 = the neighbouring frame's edge block):
+    #   f = 0:  keys are frames {0, 1}; only q-block 62 reaches past frame 0
+    #           (block 63, frame 1's first)                       -> 3969 + 1
+    #   f = 1:  keys {0, 1, 2}; q-block 0 adds 2 (block 62 is frame 0),
+    #           q-blocks 1..62 add 3 each                         -> 3969 + 188
+    #   f = 20: keys {0, 19, 20}; q-block 62 adds 2 (no frame 21),
+    #           q-blocks 0..61 add 3 each                         -> 3969 + 188
+    #   f = 2..19: 3 each for all 63 q-blocks                     -> 3969 + 189
+    tpf = 4032
+    rows = torch.stack([torch.arange(f * tpf, (f + 1) * tpf) for f in range(21)])
+    keys = [torch.cat([torch.arange(x * tpf, (x + 1) * tpf)
+                       for x in sorted({0, f - 1, f, f + 1} & set(range(21)))]) for f in range(21)]
+    p = IndexedPlan.create(rows, keys, 21 * tpf, protected_ranges=((0, tpf),), local_tokens=64)
+    assert sorted(set(p.key_lengths.tolist())) == [8064, 12096, 16128]
+    for f, expect in ((0, 3970), (1, 4157), (10, 4158), (19, 4158), (20, 4157)):
+        nkb = -(-len(keys[f]) // 64)
+        assert int(p.protected_blocks[f, :, :nkb].sum()) == expect
+        assert not p.protected_blocks[f, :, nkb:].any()
