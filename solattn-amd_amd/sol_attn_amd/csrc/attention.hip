@@ -109,23 +109,25 @@ __device__ __forceinline__ bf16x8 pack8(const f32x16& s, int base) {
   return as_bf16x8(pb);
 }
 
-// 16-byte global -> LDS DMA per lane: lane l reads base + lane_bytes and its
-// bytes land at lds_base + 16 l.  The wave-uniform base travels in an SGPR
-// pair (global "saddr" form) and the per-lane part is a 32-bit offset, so a
-// refill holds no 64-bit per-lane addresses in vector registers.  Issued as
-// inline assembly so that the compiler does not drain the vector memory
-// counter before every LDS read (it cannot tell the ring's buffers apart);
-// completion is awaited explicitly with wait_vmcnt before the barrier.  M0
-// (the LDS base register of the DMA) is saved and restored around it.
-__device__ __forceinline__ void dma16(const uint16_t* base, uint32_t lane_bytes, uint32_t lds_base) {
-  const uint64_t b = reinterpret_cast<uint64_t>(base);
-  // Wave-uniform by construction; readfirstlane makes that visible to the
-  // compiler.  It returns a signed int: each half goes through uint32_t so
-  // that the low word is zero-extended, never sign-extended into the high word.
-  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(b)));
-  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(b >> 32)));
-  const uint64_t sbase = (uint64_t(hi) << 32) | uint64_t(lo);
-  const uint32_t m = uint32_t(__builtin_amdgcn_readfirstlane(lds_base));
+// Wave-uniform copy of a 64-bit value, in an SGPR pair.  readfirstlane
+// returns a signed int: each half goes through uint32_t so that the low word
+// is zero-extended, never sign-extended into the high word.
+__device__ __forceinline__ uint64_t uniform64(uint64_t x) {
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(x)));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(x >> 32)));
+  return (uint64_t(hi) << 32) | uint64_t(lo);
+}
+
+// 16-byte global -> LDS DMA per lane: lane l reads sbase + lane_bytes and its
+// bytes land at LDS address m + 16 l; sbase and m are wave-uniform.  The base
+// travels in an SGPR pair (global "saddr" form) and the per-lane part is a
+// 32-bit offset, so a refill holds no 64-bit per-lane addresses in vector
+// registers.  Issued as inline assembly so that the compiler does not drain
+// the vector memory counter before every LDS read (it cannot tell the ring's
+// buffers apart); completion is awaited explicitly with wait_vmcnt before the
+// barrier.  M0 (the LDS base register of the DMA) is saved and restored
+// around it.
+__device__ __forceinline__ void dma16(uint64_t sbase, uint32_t lane_bytes, uint32_t m) {
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
@@ -143,40 +145,58 @@ __device__ __forceinline__ uint32_t lds_address(const void* p) {
 }
 
 // DMA of one K + V^T tile pair (contiguous in HBM) into an LDS buffer, in
-// kRounds rounds of one 16-byte chunk per lane.  A refill can be issued
-// whole, or a few rounds at a time between a wave's score MFMAs, so that
-// the wave's in-order instruction stream does not stall on a burst of DMA
-// issues.  Every round must be issued exactly once per refill.
+// kRounds rounds of one 16-byte chunk per lane: round r moves the 1 KB piece
+// of wave w at byte offset 16 (r NT + 64 w).  A refill can be issued whole,
+// or a few rounds at a time between a wave's score MFMAs, so that the wave's
+// in-order instruction stream does not stall on a burst of DMA issues.
+// Every round must be issued exactly once per refill.  Rounds are
+// unconditional (no branch splits the MFMA schedule): a stream with no
+// further tile refills the slot with a tile it already read, into a slot no
+// later tile uses.
 template <int D, int NT>
 struct TileRefill {
   static constexpr int kChunks = Shape<D>::TILE / 8;  // 16-byte chunks per tile pair
   static constexpr int kRounds = kChunks / NT;
   static_assert(kChunks % NT == 0, "tile pair must split evenly over the workgroup");
-  const uint16_t* src;  // nullptr: nothing to load
-  uint16_t* dst;
-  int wave, lane;
+  uint64_t src;         // wave-uniform address of this wave's first chunk
+  uint32_t lds;         // wave-uniform LDS address of the same chunk
+  uint32_t lane_bytes;  // 16 * lane
+
+  __device__ __forceinline__ TileRefill(const uint16_t* tile, uint32_t dst_lds, int wave, int lane)
+      : src(uniform64(reinterpret_cast<uint64_t>(tile) + uint64_t(wave) * (kWave * 16))),
+        lds(uint32_t(__builtin_amdgcn_readfirstlane(dst_lds + uint32_t(wave) * (kWave * 16)))),
+        lane_bytes(uint32_t(lane) * 16u) {}
 
   __device__ __forceinline__ void round(int r) const {
-    if (src) {
-      const int chunk = r * NT + wave * kWave;  // first chunk of this wave's 1 KB piece
-      dma16(src + chunk * 8, uint32_t(lane) * 16u, lds_address(dst + chunk * 8));
-    }
+    // The round's offset passes through an empty asm so that it is formed
+    // here from an immediate, not kept live in registers of its own across
+    // the whole stream.
+    uint32_t off = uint32_t(r) * (NT * 16);
+    asm volatile("" : "+s"(off));
+    dma16(src + off, lane_bytes, lds + off);
   }
   __device__ __forceinline__ void all() const {
 #pragma unroll
     for (int r = 0; r < kRounds; ++r) round(r);
   }
-  // The rounds that belong after k-step ks of a KT-step score loop.
-  template <int KT>
-  __device__ __forceinline__ void after_kstep(int ks) const {
+  // The rounds that belong after step k of an N-step schedule.
+  template <int N>
+  __device__ __forceinline__ void after_step(int k) const {
 #pragma unroll
-    for (int r = ks * kRounds / KT; r < (ks + 1) * kRounds / KT; ++r) round(r);
+    for (int r = k * kRounds / N; r < (k + 1) * kRounds / N; ++r) round(r);
   }
 };
 
+// A refill with nothing to load (single-slot ring).
+struct NoRefill {
+  __device__ __forceinline__ void all() const {}
+  template <int N>
+  __device__ __forceinline__ void after_step(int) const {}
+};
+
 template <int D, int NT>
-__device__ __forceinline__ void tile_dma(const uint16_t* src, uint16_t* dst, int wave, int lane) {
-  TileRefill<D, NT>{src, dst, wave, lane}.all();
+__device__ __forceinline__ void tile_dma(const uint16_t* src, uint32_t dst_lds, int wave, int lane) {
+  TileRefill<D, NT>(src, dst_lds, wave, lane).all();
 }
 
 template <int N>
@@ -198,151 +218,229 @@ __device__ __forceinline__ int fresh(int x) {
   return x;
 }
 
-// Scores of key halves [kh0, kh0 + NH) of an LDS tile pair against this
-// wave's 32 queries, plus the V^T fragments for the P V^T product.  The K
-// fragments are read and multiplied first; the V^T fragments are read after
-// the last score MFMA has issued (a scheduling barrier keeps them there), so
-// they reuse the K fragments' registers and arrive during the softmax.
-template <int D, int NH, typename Refill>
-__device__ __forceinline__ void tile_scores(const uint16_t* buf, int kh0,
-                                            const bf16x8 (&qf)[Shape<D>::KT], int col, int hh,
-                                            f32x16 (&p)[NH], u32x4 (&va)[NH][2][Shape<D>::DT],
-                                            const Refill& refill) {
-  using S = Shape<D>;
-  using TL = TileLayout<D>;
-  const uint16_t* kt_lds = buf;
-  const uint16_t* vt_lds = buf + TL::kElems;
-  col = fresh(col);
-  hh = fresh(hh);
-  u32x4 ka[NH][S::KT];
-#pragma unroll
-  for (int ks = 0; ks < S::KT; ++ks)
-#pragma unroll
-    for (int t = 0; t < NH; ++t)
-      ka[t][ks] = *reinterpret_cast<const u32x4*>(kt_lds + TL::k_offset(32 * (kh0 + t) + col, 2 * ks + hh));
-#pragma unroll
-  for (int t = 0; t < NH; ++t) p[t] = zero16();
-#pragma unroll
-  for (int ks = 0; ks < S::KT; ++ks) {
-#pragma unroll
-    for (int t = 0; t < NH; ++t) p[t] = mfma32x32x16(as_bf16x8(ka[t][ks]), qf[ks], p[t]);
-    refill.template after_kstep<S::KT>(ks);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int t = 0; t < NH; ++t)
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const int g = 8 * (kh0 + t) + 4 * c + hh;  // 4-key group of keys 32(kh0+t) + 16c + 4hh
-#pragma unroll
-      for (int dt = 0; dt < S::DT; ++dt) {
-        const int d = dt * 32 + col;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vt_lds + TL::vt_offset(d, g));
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vt_lds + TL::vt_offset(d, g + 2));
-        va[t][c][dt] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      }
-    }
-}
-
-// Lazy online softmax + P V for one 64-key tile (two 32-key halves) of raw
-// scores s (-inf = absent); c = scale * log2(e) moves them to log2 units
-// inside the exponent.  The wave's running max m (log2 units) moves only when
-// some query's tile max exceeds it by more than kRescaleSlack; otherwise the
-// tile's probabilities exp2(s c - m) * weight may exceed 1 by up to
-// 2^kRescaleSlack (times the weight), which FP32 sums and BF16 products carry
-// at unchanged relative precision.  acc and den always share m, so
-// O = acc / den is unaffected.  Without a rescale the second half's exp2 work
-// does not depend on the first half's P V products, and the schedule
-// interleaves the two (one MFMA, then VALU work, repeated).
-constexpr float kRescaleSlack = 8.f;
-
-template <int D, typename Weight>
-__device__ __forceinline__ void softmax_pv(State<D>& st, f32x16 (&s)[2],
-                                           const u32x4 (&va)[2][2][Shape<D>::DT], float c,
-                                           Weight weight) {
-  constexpr int DT = Shape<D>::DT;
-  float mx = kNegInf;
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[t][e]);
-  mx = pair_max(mx) * c;
-  if (__builtin_amdgcn_ballot_w64(mx > st.m + kRescaleSlack)) {
-    const float mnew = fmaxf(st.m, mx);
-    const float alpha = fast_exp2(st.m - (mnew == kNegInf ? 0.f : mnew));
-    st.den *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) st.acc[dt] *= alpha;
-    st.m = mnew;
-  }
-  const float neg_m = st.m == kNegInf ? 0.f : -st.m;
-  float lsum = 0.f;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float pe = fast_exp2(fmaf(s[t][e], c, neg_m)) * weight(t, e);
-      s[t][e] = pe;
-      lsum += pe;
-    }
-    const bf16x8 b0 = pack8(s[t], 0), b1 = pack8(s[t], 8);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) st.acc[dt] = mfma32x32x16(as_bf16x8(va[t][0][dt]), b0, st.acc[dt]);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) st.acc[dt] = mfma32x32x16(as_bf16x8(va[t][1][dt]), b1, st.acc[dt]);
-  }
-  st.den += lsum;
-#pragma unroll
-  for (int i = 0; i < 2 * DT; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // then up to six VALU
-  }
-}
-
-// Key row (inside a 64-row tile) of element e of this lane's 32-key half t.
+// Key row (inside a 64-row tile) of element e of this lane's 32-key half t:
+// in the 32x32 MFMA result layout, lane half hh holds rows
+// 8 (e / 4) + 4 hh + e % 4 of each 32-row half.
 __device__ __forceinline__ int tile_row(int t, int e, int hh) {
   return 32 * t + 8 * (e >> 2) + 4 * hh + (e & 3);
 }
 
-// What a wave carries from the LDS phase of a tile (score MFMAs issued,
-// V^T fragments read) to its compute phase.
+// Lazy online softmax: the wave's running max m (log2 units) moves only when
+// some query's max exceeds it by more than kRescaleSlack.  Otherwise the
+// probabilities exp2(s c - m) may exceed 1 by up to 2^kRescaleSlack, which
+// FP32 sums and BF16 products carry at unchanged relative precision; acc and
+// den always share m, so O = acc / den is unaffected.  The common case has
+// no data-dependent branch, so a half's softmax can be spread between
+// matrix-core instructions.
+constexpr float kRescaleSlack = 8.f;
+
+// Materialises a value at this point of the instruction stream, so that the
+// work producing it stays ahead of a following branch (where the scheduler
+// can overlap it with matrix-core work) instead of being sunk past it.
+template <typename T>
+__device__ __forceinline__ void pin(T& x) {
+  asm volatile("" : "+v"(x));
+}
+
+// Softmax of one 32-key half of raw scores s (absent keys -inf; c = scale *
+// log2(e)), in 8 stages that a caller places between MFMAs: max; the
+// wave-uniform rescale decision, new max and alpha; 4 x 4 probabilities
+// exp2(s c - m); BF16 packing into pb[16-key c]; den update.  The caller
+// multiplies acc by alpha when `rescale` is set.
 template <int D>
-struct TileFrags {
-  f32x16 p[2];                   // raw scores of the two 32-key halves
-  u32x4 va[2][2][Shape<D>::DT];  // V^T fragments
+struct HalfSoftmax {
+  f32x16 s;
+  float mx, alpha, neg_m, lsum;
+  bool rescale;
+  bf16x8 pb[2];
+
+  __device__ __forceinline__ void stage(int k, State<D>& st, float c) {
+    if (k == 0) {
+      mx = kNegInf;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[e]);
+    } else if (k == 1) {
+      mx = pair_max(mx) * c;
+      rescale = __builtin_amdgcn_ballot_w64(mx > st.m + kRescaleSlack) != 0;
+      const float mnew = rescale ? fmaxf(st.m, mx) : st.m;
+      alpha = fast_exp2(st.m - (mnew == kNegInf ? 0.f : mnew));  // 1 without a rescale (0 before any key)
+      st.m = mnew;
+      neg_m = mnew == kNegInf ? 0.f : -mnew;
+      lsum = 0.f;
+    } else if (k < 6) {
+#pragma unroll
+      for (int e = 4 * (k - 2); e < 4 * (k - 1); ++e) {
+        const float pe = fast_exp2(fmaf(s[e], c, neg_m));
+        s[e] = pe;
+        lsum += pe;
+      }
+    } else if (k == 6) {
+      pb[0] = pack8(s, 0);
+      pb[1] = pack8(s, 8);
+      pin(pb[0]);
+      pin(pb[1]);
+    } else {
+      st.den = st.den * alpha + lsum;
+      pin(st.den);
+    }
+  }
+  // Part k of n (n = 4 or 8) of the stages.
+  template <int N>
+  __device__ __forceinline__ void part(int k, State<D>& st, float c) {
+#pragma unroll
+    for (int i = k * 8 / N; i < (k + 1) * 8 / N; ++i) stage(i, st, c);
+  }
 };
 
-// Exact 64-key block j: tail mask, online softmax, P V.
+// acc *= alpha, in place (the accumulator keeps its registers on both sides
+// of the rare rescale branch instead of being copied).
 template <int D>
-__device__ __forceinline__ void exact_finish(TileFrags<D>& f, int j, int tk, float scale_log2, int hh,
-                                             State<D>& st) {
-  if ((j + 1) * kBlock > tk) {  // tail block: keys past the end are absent
+__device__ __forceinline__ void rescale_acc(State<D>& st, float alpha) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+  for (int dt = 0; dt < Shape<D>::DT; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        if (j * kBlock + tile_row(t, e, hh) >= tk) f.p[t][e] = kNegInf;
+    for (int e = 0; e < 16; ++e) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(st.acc[dt][e]) : "v"(alpha));
+}
+
+// K fragment of k-step ks for this lane's key row of half t.
+template <int D>
+__device__ __forceinline__ u32x4 k_frag(const uint16_t* buf, int t, int ks, int col, int hh) {
+  return *reinterpret_cast<const u32x4*>(buf + TileLayout<D>::k_offset(32 * t + col, 2 * ks + hh));
+}
+
+// V^T fragment [16-key c4][feature tile dt] of half t: one 16-byte chunk.
+template <int D>
+__device__ __forceinline__ u32x4 v_frag(const uint16_t* buf, int t, int c4, int dt, int col, int hh) {
+  using TL = TileLayout<D>;
+  return *reinterpret_cast<const u32x4*>(buf + TL::kElems + TL::vt_chunk(dt * 32 + col, 4 * t + 2 * c4 + hh));
+}
+
+// Ends a scheduling chunk: nothing moves across it, so the hand-placed
+// interleave of matrix-core, LDS, DMA and VALU work below is kept.
+__device__ __forceinline__ void chunk_end() { __builtin_amdgcn_sched_barrier(0); }
+
+// One 64-key tile, software-pipelined over its two 32-key halves inside the
+// wave so that the VALU softmax work overlaps the MFMAs:
+//   chunk 0        half 0's K reads
+//   chunks 1..KT   half 0's score MFMAs; half 1's K reads
+//   next KT        half 1's score MFMAs; half 0's softmax; half 0's V^T reads
+//   [rescale]
+//   next 2 DT      half 0's P V MFMAs; half 1's softmax; half 1's V^T reads
+//   [rescale]      half 1's P V MFMAs
+// The refill's DMA rounds are spread over the 2 KT score chunks.  Scores
+// start from bias(t) when BIASED (-inf drops a key, log2(len) / c adds a
+// centroid's ln(len) logit term), else from 0.
+template <int D, bool BIASED, typename Bias, typename Refill>
+__device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
+                                            const bf16x8 (&qf)[Shape<D>::KT], int col, int hh, float c,
+                                            Bias bias, const Refill& refill) {
+  constexpr int KT = Shape<D>::KT, DT = Shape<D>::DT;
+  static_assert(KT == 2 * DT, "score and P V chunk counts match");
+  col = fresh(col);
+  hh = fresh(hh);
+  u32x4 k0[KT], k1[KT];
+#pragma unroll
+  for (int ks = 0; ks < KT; ++ks) k0[ks] = k_frag<D>(buf, 0, ks, col, hh);
+  HalfSoftmax<D> h0, h1;
+  h0.s = BIASED ? bias(0) : zero16();
+  chunk_end();
+#pragma unroll
+  for (int ks = 0; ks < KT; ++ks) {
+    h0.s = mfma32x32x16(as_bf16x8(k0[ks]), qf[ks], h0.s);
+    k1[ks] = k_frag<D>(buf, 1, ks, col, hh);
+    refill.template after_step<2 * KT>(ks);
+    chunk_end();
   }
-  softmax_pv<D>(st, f.p, f.va, scale_log2, UnitWeight{});
+  u32x4 va[2][DT];
+#pragma unroll
+  for (int ks = 0; ks < KT; ++ks) {
+    if (ks == 0) h1.s = BIASED ? bias(1) : zero16();
+    h1.s = mfma32x32x16(as_bf16x8(k1[ks]), qf[ks], h1.s);
+    h0.template part<KT>(ks, st, c);
+    if (ks >= KT / 2) {  // two of half 0's 2 DT = KT V^T fragments per chunk
+#pragma unroll
+      for (int f = 2 * (ks - KT / 2); f < 2 * (ks - KT / 2) + 2; ++f)
+        va[f / DT][f % DT] = v_frag<D>(buf, 0, f / DT, f % DT, col, hh);
+    }
+    refill.template after_step<2 * KT>(KT + ks);
+    chunk_end();
+  }
+  if (h0.rescale) rescale_acc<D>(st, h0.alpha);
+  u32x4 vb[2][DT];
+#pragma unroll
+  for (int f = 0; f < 2 * DT; ++f) {
+    const int c4 = f / DT, dt = f % DT;
+    st.acc[dt] = mfma32x32x16(as_bf16x8(va[c4][dt]), h0.pb[c4], st.acc[dt]);
+    vb[c4][dt] = v_frag<D>(buf, 1, c4, dt, col, hh);
+    h1.template part<2 * DT>(f, st, c);
+    chunk_end();
+  }
+  if (h1.rescale) rescale_acc<D>(st, h1.alpha);
+#pragma unroll
+  for (int f = 0; f < 2 * DT; ++f) {
+    const int c4 = f / DT, dt = f % DT;
+    st.acc[dt] = mfma32x32x16(as_bf16x8(vb[c4][dt]), h1.pb[c4], st.acc[dt]);
+  }
+}
+
+struct NoBias {
+  __device__ __forceinline__ f32x16 operator()(int) const { return zero16(); }
+};
+
+// A full exact block (every key present).
+template <int D, typename Refill>
+__device__ __forceinline__ void full_tile(State<D>& st, const uint16_t* buf,
+                                          const bf16x8 (&qf)[Shape<D>::KT], int col, int hh, float c,
+                                          const Refill& refill) {
+  tile_attend<D, false>(st, buf, qf, col, hh, c, NoBias{}, refill);
+}
+
+// Exact block j: a full block, or the tail block whose keys at or past tk
+// start at -inf.  Only a stream's last exact tile can be the tail block.
+template <int D, typename Refill>
+__device__ __forceinline__ void exact_tile(State<D>& st, const uint16_t* buf, int j, int tk,
+                                           const bf16x8 (&qf)[Shape<D>::KT], int col, int hh, float c,
+                                           const Refill& refill) {
+  if ((j + 1) * kBlock <= tk) {
+    full_tile<D>(st, buf, qf, col, hh, c, refill);
+  } else {
+    const int lane_keys = fresh(tk - j * kBlock - 4 * hh);  // keys from this lane's first row on
+    tile_attend<D, true>(st, buf, qf, col, hh, c,
+                         [&](int t) {
+                           f32x16 bias;
+#pragma unroll
+                           for (int e = 0; e < 16; ++e)
+                             bias[e] = tile_row(t, e, 0) < lane_keys ? 0.f : kNegInf;
+                           return bias;
+                         },
+                         refill);
+  }
 }
 
 // Centroid tile ct: the block centroids 64 ct + r whose bit r is set in
-// `approx` contribute logit q . Kc_j + ln(len_j) and value Vc_j; the length
-// enters as a weight on exp2(s - m).
-template <int D>
-__device__ __forceinline__ void centroid_finish(TileFrags<D>& f, int ct, uint64_t approx, int tk,
-                                                float scale_log2, int hh, State<D>& st) {
-  // Row of element e of half t = 4 hh + (a compile-time constant): only the
-  // lane's share is formed at run time, so nothing per element stays live.
+// `approx` contribute logit q . Kc_j + ln(len_j) and value Vc_j: their scores
+// start at log2(len_j) / c (c = scale * log2(e)), the others at -inf.  Only
+// the lane's share of the row index is formed at run time.
+template <int D, typename Refill>
+__device__ __forceinline__ void centroid_tile(State<D>& st, const uint16_t* buf, int ct, uint64_t approx,
+                                              int tk, const bf16x8 (&qf)[Shape<D>::KT], int col, int hh,
+                                              float c, const Refill& refill) {
   const uint64_t lane_approx = approx >> (4 * hh);
-  const int lane_tokens = tk - kBlock * (kBlock * ct + 4 * hh);  // keys from the lane's first block on
+  const int lane_tokens = fresh(tk - kBlock * (kBlock * ct + 4 * hh));  // keys from the lane's first block on
+  const float inv_c = 1.f / c;
+  tile_attend<D, true>(st, buf, qf, col, hh, c,
+                       [&](int t) {
+                         f32x16 bias;
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      if (!((lane_approx >> tile_row(t, e, 0)) & 1u)) f.p[t][e] = kNegInf;
-  auto len = [&](int t, int e) { return float(min(kBlock, lane_tokens - kBlock * tile_row(t, e, 0))); };
-  softmax_pv<D>(st, f.p, f.va, scale_log2, len);
+                         for (int e = 0; e < 16; ++e) {
+                           const int row = tile_row(t, e, 0);
+                           const int len = min(kBlock, lane_tokens - kBlock * row);
+                           bias[e] = ((lane_approx >> row) & 1u)
+                                         ? __builtin_amdgcn_logf(float(len)) * inv_c : kNegInf;
+                         }
+                         return bias;
+                       },
+                       refill);
 }
 
 template <int D>
@@ -387,43 +485,79 @@ __device__ __forceinline__ void lds_barrier() {
 // Streams `count` tiles through an R-slot LDS ring: while tile i is on the
 // matrix cores, the DMA of tiles i+1 .. i+R-1 is in flight.  One barrier per
 // tile: after it, tile i is visible to every wave and every wave has finished
-// tile i-1, whose slot then receives tile i+R-1.  Per tile,
-// load(buf, id, refill) reads this wave's fragments from LDS, issues the score
-// MFMAs and, between them, the rounds of that refill DMA (or all of them at
-// once when it has no scores to compute); compute(frags, id) finishes the
-// tile from registers.  `next()` yields tile ids in
-// order and is evaluated identically by every thread; source(id) is the
-// tile's HBM address.  Two streams over the same ring are separated by a
-// barrier.
-template <int D, int NT, int R, typename Next, typename Source, typename Load, typename Compute>
+// tile i-1, whose slot then receives tile i+R-1 (or, past the last tile, tile
+// i again, read by nobody).  process(buf, id, refill) consumes tile i and
+// issues that refill's DMA rounds (between its score MFMAs, or all at once
+// when it has nothing to compute); the last tile goes to last(buf, id,
+// refill) instead, so that the loop body holds only the common case (an
+// exact stream's last tile may be a partial block).  `next()` yields tile ids
+// in order and is evaluated identically by every thread; source(id) is the
+// tile's HBM address.  R = 1: one slot, refilled after a barrier (latency
+// hidden by the other workgroups of the CU).  Two streams over the same ring
+// are separated by a barrier.
+template <int D, int NT, int R, typename Next, typename Source, typename Process, typename Last>
 __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next, Source source,
-                                            Load load, Compute compute, int wave, int lane) {
+                                            Process process, Last last, int wave, int lane) {
   using S = Shape<D>;
   constexpr int kRounds = S::TILE / 8 / NT;
-  static_assert(R >= 2 && R <= 4 && (R & (R - 1)) == 0, "ring depth 2 or 4");
-  static_assert((R - 2) * kRounds <= 63, "vmcnt range");
+  static_assert(R >= 1 && R <= 4 && (R & (R - 1)) == 0, "ring depth 1, 2 or 4");
+  static_assert(R < 2 || (R - 2) * kRounds <= 63, "vmcnt range");
   if (count <= 0) return;
-  int ids[R - 1];  // tiles i .. i+R-2 (uniform); shifted each iteration
+  const uint32_t ring_lds = lds_address(ring);
+  if constexpr (R == 1) {
+    for (int i = 0; i < count; ++i) {
+      const int id = next();
+      TileRefill<D, NT>(source(id), ring_lds, wave, lane).all();
+      wait_vmcnt<0>();
+      ring_barrier();
+      if (i + 1 < count) {
+        if (process.selected(id)) process.hit(ring, id, NoRefill{});
+        else process.miss(ring, id, NoRefill{});
+      } else {
+        last(ring, id, NoRefill{});
+      }
+      lds_barrier();
+    }
+    return;
+  }
+  int ids[R > 1 ? R - 1 : 1];  // tiles i .. i+R-2 (uniform); shifted each iteration
 #pragma unroll
   for (int s = 0; s < R - 1; ++s) {
     ids[s] = s < count ? next() : 0;
-    if (s < count) tile_dma<D, NT>(source(ids[s]), ring + s * S::TILE, wave, lane);
+    if (s < count) tile_dma<D, NT>(source(ids[s]), ring_lds + uint32_t(s * S::TILE * 2), wave, lane);
   }
-  for (int i = 0; i < count; ++i) {
+  auto step = [&](int i, auto&& fn) {
     wait_ahead<kRounds>(min(R - 2, count - 1 - i));
-    ring_barrier();
+    lds_barrier();
     const int id = ids[0];
 #pragma unroll
     for (int s = 0; s < R - 2; ++s) ids[s] = ids[s + 1];
-    TileRefill<D, NT> refill{nullptr, ring + ((i + R - 1) & (R - 1)) * S::TILE, wave, lane};
+    int idn = id;
     if (i + R - 1 < count) {
-      const int idn = next();
+      idn = next();
       ids[R - 2] = idn;
-      refill.src = source(idn);
     }
-    auto frags = load(ring + (i & (R - 1)) * S::TILE, id, refill);
-    compute(frags, id);
+    fn(ring + (i & (R - 1)) * S::TILE, id,
+       TileRefill<D, NT>(source(idn), ring_lds + uint32_t(((i + R - 1) & (R - 1)) * S::TILE * 2), wave, lane));
+  };
+  int i = 0;
+  while (i < count - 1) {
+    if (process.selected(ids[0])) {
+      do {
+        step(i, process.hit);
+        ++i;
+      } while (i < count - 1 && process.selected(ids[0]));
+    } else {
+      do {
+        step(i, process.miss);
+        ++i;
+      } while (i < count - 1 && !process.selected(ids[0]));
+    }
   }
+  step(count - 1, last);
+  // The last refills were issued after the last wait: drain them before the
+  // ring is reused or the workgroup exits.
+  wait_vmcnt<0>();
 }
 
 // Approximated blocks of centroid tile ct for one query block: valid blocks
@@ -479,6 +613,22 @@ struct RangeCursor {
 }  // namespace
 
 
+// Query block of slot s (= group index * G + member) when group members are
+// query blocks `stride` apart: within each run of 2 * stride blocks, block i
+// pairs with block i + stride; blocks past the last full run keep their slot.
+// A bijection on [0, n); slots >= n stay >= n (no query block).
+__device__ __forceinline__ int slot_block(int s, int n, int stride) {
+  if (stride <= 0) return s;
+  const int run = 2 * stride;
+  if (s >= (n / run) * run) return s;
+  const int w = s % run;
+  return (s / run) * run + (w >> 1) + (w & 1) * stride;
+}
+
+#ifndef SOL_PAIR_STRIDE
+#define SOL_PAIR_STRIDE 0
+#endif
+
 // __launch_bounds__ second argument: minimum waves per SIMD.  Two waves per
 // SIMD leave each wave 256 VGPRs: the exact path keeps the 64-register
 // accumulator, 32 registers of Q fragments and 64 of K or V fragments live.
@@ -505,8 +655,8 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
   const int col = lane & 31, hh = lane >> 5;
   const int qg = wave >> 1, qh = wave & 1;  // query block in the group, query half
   const int lt = tid & 127;                  // thread index inside the query block's 2 waves
-  const int qb0 = task.tile * G;
-  const int qb = qb0 + qg;
+  const int qb0 = task.tile * G;  // first slot of this group
+  const int qb = slot_block(qb0 + qg, p.NQB, SOL_PAIR_STRIDE);
   const bool live = qb < p.NQB;
   const int tk = batch_tokens(p.klen, b, p.Tk);  // this entry's key tokens
   const int nkb = (tk + kBlock - 1) / kBlock;      // its key blocks (<= p.NKB, the buffer stride)
@@ -516,7 +666,7 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
   // 1. Q tiles -> LDS -> fragments.
   for (int idx = tid; idx < G * kBlock * S::DC; idx += NT) {
     const int r = idx / S::DC, c = idx % S::DC;
-    const int t = qb0 * kBlock + r;
+    const int t = slot_block(qb0 + r / kBlock, p.NQB, SOL_PAIR_STRIDE) * kBlock + r % kBlock;
     const u32x4 x = t < p.Tq ? load16(p.q.row(b, t, h) + 8 * c) : zero_u32x4();
     *reinterpret_cast<u32x4*>(ring + r * S::KS + 8 * c) = x;
   }
@@ -578,20 +728,20 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
     for (int i = tid; i < G * nwords; i += NT) {
       const int g = i / nwords, w = i % nwords;
       const int nvalid = min(32, nkb - 32 * w);
-      s_mask[g][w] = qb0 + g < p.NQB ? (nvalid == 32 ? ~0u : ((1u << nvalid) - 1u)) : 0u;
+      s_mask[g][w] = slot_block(qb0 + g, p.NQB, SOL_PAIR_STRIDE) < p.NQB
+                         ? (nvalid == 32 ? ~0u : ((1u << nvalid) - 1u)) : 0u;
     }
     if (live && p.dbg_selected)
       for (int j = lt; j < nkb; j += 128) p.dbg_selected[dbg_row + j] = 1;
     __syncthreads();
   } else {
-    // 3. Centroid pass.  Load phase: routing of the tile's 64 blocks for every
+    // 3. Centroid pass.  Per tile: routing of the tile's 64 blocks for every
     // query block of the group -- wave w scores blocks 32 (w & 1) + (lane & 31)
     // of query block w >> 1 over feature half lane >> 5, the halves summed
-    // across the lane pair -- into the LDS bitmask, and this wave's centroid
-    // scores.  Compute phase (after the barrier publishes the mask): the
-    // approximated blocks' contributions.
+    // across the lane pair -- into the LDS bitmask; a barrier publishes the
+    // mask; then the approximated blocks' contributions.
     const uint16_t* ctiles = p.ctiles + head * p.NCT * S::TILE;
-    auto load = [&](const uint16_t* buf, int ct, const TileRefill<D, NT>& refill) {
+    auto process = [&](const uint16_t* buf, int ct, const auto& refill) {
       const int r = fresh(32 * qh + col);  // centroid row inside the tile
       const int j = kBlock * ct + r;
       bool sel = false;
@@ -621,24 +771,18 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
       }
       const uint64_t bal = __ballot(sel);
       if (lane == 0) s_mask[qg][2 * ct + qh] = uint32_t(bal);
-      TileFrags<D> f;
-      if (live) {
-        tile_scores<D, 2>(buf, 0, qf, col, hh, f.p, f.va, refill);
-      } else {
-        refill.all();
-      }
-      lds_barrier();  // publishes the mask words for compute
-      return f;
+      lds_barrier();  // publishes the mask words
+      // Branch-free: a tile with no approximated block for this query block
+      // (or a query block past the end) has every score at -inf and adds
+      // nothing.
+      const uint64_t approx = live ? tile_approx(s_mask[qg], ct, nkb) : 0ull;
+      centroid_tile<D>(st, buf, ct, approx, tk, qf, col, hh, scale_log2, refill);
     };
-    auto compute = [&](TileFrags<D>& f, int ct) {
-      if (live) {
-        const uint64_t approx = tile_approx(s_mask[qg], ct, nkb);
-        if (approx) centroid_finish<D>(f, ct, approx, tk, scale_log2, hh, st);
-      }
-    };
+    auto always = [](int) { return true; };
+    struct { decltype(always) selected; decltype(process) hit; decltype(process) miss; } cruns{always, process, process};
     tile_stream<D, NT, R>(ring, nct, RangeCursor{0},
-                          [&](int ct) { return ctiles + int64_t(ct) * S::TILE; }, load, compute, wave,
-                          lane);
+                          [&](int ct) { return ctiles + int64_t(ct) * S::TILE; }, cruns, process,
+                          wave, lane);
     lds_barrier();  // every wave is done with the ring's centroid tiles
   }
   if (live && p.counts && lt == 0) {
@@ -647,24 +791,25 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
     p.counts[(int64_t(b) * p.NQB + qb) * p.H + h] = nsel;
   }
 
-  // 4. Exact pass over the union of the group's selected blocks.
+  // 4. Exact pass over the union of the group's selected blocks.  Only the
+  // stream's last tile can be the partial tail block.
   UnionCursor<G> cursor{&s_mask[0][0], kMaskWords, nkb};
   const int count = cursor.count();
   const uint32_t* my_mask = s_mask[qg];
   const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
+  auto sel = [&](int j) { return ((my_mask[j >> 5] >> (j & 31)) & 1u) != 0; };
+  auto hit = [&](const uint16_t* buf, int j, const auto& refill) { full_tile<D>(st, buf, qf, col, hh, scale_log2, refill); };
+  auto miss = [&](const uint16_t* buf, int j, const auto& refill) { refill.all(); };
+  struct { decltype(sel) selected; decltype(hit) hit; decltype(miss) miss; } runs{sel, hit, miss};
   tile_stream<D, NT, R>(
       ring, count, cursor, [&](int j) { return tiles + int64_t(j) * S::TILE; },
-      [&](const uint16_t* buf, int j, const TileRefill<D, NT>& refill) {
-        TileFrags<D> f;
+      runs,
+      [&](const uint16_t* buf, int j, const auto& refill) {
         if ((my_mask[j >> 5] >> (j & 31)) & 1u) {
-          tile_scores<D, 2>(buf, 0, qf, col, hh, f.p, f.va, refill);
+          exact_tile<D>(st, buf, j, tk, qf, col, hh, scale_log2, refill);
         } else {
           refill.all();
         }
-        return f;
-      },
-      [&](TileFrags<D>& f, int j) {
-        if ((my_mask[j >> 5] >> (j & 31)) & 1u) exact_finish<D>(f, j, tk, scale_log2, hh, st);
       },
       wave, lane);
 
@@ -712,14 +857,18 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   const int tk = p.Tk;
   const float scale_log2 = p.scale_log2;
   const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
+  auto always = [](int) { return true; };
+  auto hit = [&](const uint16_t* buf, int, const auto& refill) {
+        full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
+      };
+  struct { decltype(always) selected; decltype(hit) hit; decltype(hit) miss; } runs{always, hit, hit};
   tile_stream<D, NT, 2>(
       ring, p.NKB, RangeCursor{0}, [&](int j) { return tiles + int64_t(j) * S::TILE; },
-      [&](const uint16_t* buf, int, const TileRefill<D, NT>& refill) {
-        TileFrags<D> f;
-        tile_scores<D, 2>(buf, 0, qf, col, hh, f.p, f.va, refill);
-        return f;
+      runs,
+      [&](const uint16_t* buf, int j, const auto& refill) {
+        exact_tile<D>(st, buf, j, tk, qf, col, hh, scale_log2, refill);
       },
-      [&](TileFrags<D>& f, int j) { exact_finish<D>(f, j, tk, scale_log2, hh, st); }, wave, lane);
+      wave, lane);
   store_output<D>(p, b, h, q0 + myq, hh, st);
 }
 

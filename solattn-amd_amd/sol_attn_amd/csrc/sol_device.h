@@ -39,8 +39,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return __builtin_bit_cast(uint16_t, h);
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> two round-to-nearest-even bf16 in one v_cvt_pk_bf16_f32
+// (lo in bits 0..15).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
@@ -108,10 +114,14 @@ __device__ __forceinline__ void transpose8x8(const u32x4 (&in)[8], u32x4 (&out)[
 //             s_k(r) = r & 15 for 256-byte rows (D = 128) and (r >> 1) & 7 for
 //             128-byte rows (D = 64); 16 consecutive rows (one 16-lane phase of
 //             a ds_read_b128) then cover all banks.
-//   V^T tile: 8-byte group g (4 keys) of feature row d sits at group
-//             g ^ (d & 15) ^ ((d >> 4) & 1): 16 consecutive rows use 16
-//             distinct groups, and 32 consecutive rows use distinct
-//             (row parity, group) pairs.
+//   V^T tile: a feature row (64 keys, 128 bytes) is 8 chunks of 16 bytes, one
+//             per MFMA A fragment: chunk c = 4 t + 2 c4 + hh holds the 4-key
+//             groups 8 t + 4 c4 + hh (low half) and that + 2 (high half), the
+//             keys lane half hh supplies for 16-key step c4 of 32-key half t
+//             (the k-slot order of the score MFMA's result).  Chunk c of row d
+//             sits at chunk c ^ s_v(d), s_v(d) = (d & 7) ^ ((d >> 3) & 1): 8
+//             consecutive rows use 8 distinct chunks and 16 consecutive rows
+//             distinct (row parity, chunk) pairs.
 // Keys past the end of the sequence are zero in both tiles.
 template <int D>
 struct TileLayout {
@@ -120,8 +130,13 @@ struct TileLayout {
     const int sw = D == 128 ? (row & 15) : ((row >> 1) & 7);
     return row * D + 8 * (chunk ^ sw);
   }
-  __device__ static __forceinline__ int vt_offset(int d, int group) {
-    return d * kBlock + 4 * (group ^ (d & 15) ^ ((d >> 4) & 1));
+  // V^T swizzle of feature row d.
+  __device__ static __forceinline__ int vt_swizzle(int d) { return (d & 7) ^ ((d >> 3) & 1); }
+  // Element offset of 16-byte fragment chunk c of feature row d.
+  __device__ static __forceinline__ int vt_chunk(int d, int c) { return d * kBlock + 8 * (c ^ vt_swizzle(d)); }
+  // Element offset of 4-key group g (keys 4 g .. 4 g + 3) of feature row d.
+  __device__ static __forceinline__ int vt_offset(int d, int g) {
+    return vt_chunk(d, 2 * (g >> 2) + (g & 1)) + 4 * ((g >> 1) & 1);
   }
 };
 

@@ -39,10 +39,11 @@ def unswizzle(tiles):
     chunks = np.arange(d // 8)[None, :]
     swz = (rows & 15) if d == 128 else ((rows >> 1) & 7)
     k_rows = kt[:, :, :, rows, chunks ^ swz].reshape(b, h, n, 64, d)
-    vt = t[:, :, :, 1].reshape(b, h, n, d, 16, 4)
+    vt = t[:, :, :, 1].reshape(b, h, n, d, 8, 2, 4)
     dd = np.arange(d)[:, None]
-    groups = np.arange(16)[None, :]
-    v_rows = vt[:, :, :, dd, groups ^ (dd & 15) ^ ((dd >> 4) & 1)].reshape(b, h, n, d, 64)
+    g = np.arange(16)[None, :]                       # 4-key group g = keys 4g .. 4g + 3
+    chunk = (2 * (g >> 2) + (g & 1)) ^ ((dd & 7) ^ ((dd >> 3) & 1))
+    v_rows = vt[:, :, :, dd, chunk, (g >> 1) & 1].reshape(b, h, n, d, 64)
     return k_rows, v_rows
 
 
