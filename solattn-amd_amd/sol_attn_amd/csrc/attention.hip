@@ -302,18 +302,25 @@ __device__ __forceinline__ void rescale_acc(State<D>& st, float alpha) {
     for (int e = 0; e < 16; ++e) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(st.acc[dt][e]) : "v"(alpha));
 }
 
-// K fragment of k-step ks for this lane's key row of half t.
+// This lane's element offsets of its MFMA operand reads inside a K + V^T
+// tile pair (see TileLayout): K fragment (t, ks) at k_row + 32 t D +
+// (k_x ^ 16 ks), V^T fragment (t, c4, dt) at kElems + v_row + 2048 dt +
+// (v_x ^ (32 t + 16 c4)); the per-read parts are immediates or one XOR-add.
 template <int D>
-__device__ __forceinline__ u32x4 k_frag(const uint16_t* buf, int t, int ks, int col, int hh) {
-  return *reinterpret_cast<const u32x4*>(buf + TileLayout<D>::k_offset(32 * t + col, 2 * ks + hh));
-}
-
-// V^T fragment [16-key c4][feature tile dt] of half t: one 16-byte chunk.
-template <int D>
-__device__ __forceinline__ u32x4 v_frag(const uint16_t* buf, int t, int c4, int dt, int col, int hh) {
-  using TL = TileLayout<D>;
-  return *reinterpret_cast<const u32x4*>(buf + TL::kElems + TL::vt_chunk(dt * 32 + col, 4 * t + 2 * c4 + hh));
-}
+struct FragLane {
+  int k_row, k_x, v_row, v_x;
+  __device__ __forceinline__ FragLane(int col, int hh)
+      : k_row(col * D),
+        k_x(TileLayout<D>::k_lane_xor(col, hh)),
+        v_row(TileLayout<D>::kElems + col * kBlock),
+        v_x(TileLayout<D>::vt_lane_xor(col, hh)) {}
+  __device__ __forceinline__ u32x4 k(const uint16_t* buf, int t, int ks) const {
+    return *reinterpret_cast<const u32x4*>(buf + k_row + 32 * t * D + (k_x ^ (16 * ks)));
+  }
+  __device__ __forceinline__ u32x4 v(const uint16_t* buf, int t, int c4, int dt) const {
+    return *reinterpret_cast<const u32x4*>(buf + v_row + 32 * kBlock * dt + (v_x ^ (32 * t + 16 * c4)));
+  }
+};
 
 // Ends a scheduling chunk: nothing moves across it, so the hand-placed
 // interleave of matrix-core, LDS, DMA and VALU work below is kept.
@@ -336,18 +343,17 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
                                             Bias bias, const Refill& refill) {
   constexpr int KT = Shape<D>::KT, DT = Shape<D>::DT;
   static_assert(KT == 2 * DT, "score and P V chunk counts match");
-  col = fresh(col);
-  hh = fresh(hh);
+  const FragLane<D> fl(fresh(col), fresh(hh));
   u32x4 k0[KT], k1[KT];
 #pragma unroll
-  for (int ks = 0; ks < KT; ++ks) k0[ks] = k_frag<D>(buf, 0, ks, col, hh);
+  for (int ks = 0; ks < KT; ++ks) k0[ks] = fl.k(buf, 0, ks);
   HalfSoftmax<D> h0, h1;
   h0.s = BIASED ? bias(0) : zero16();
   chunk_end();
 #pragma unroll
   for (int ks = 0; ks < KT; ++ks) {
     h0.s = mfma32x32x16(as_bf16x8(k0[ks]), qf[ks], h0.s);
-    k1[ks] = k_frag<D>(buf, 1, ks, col, hh);
+    k1[ks] = fl.k(buf, 1, ks);
     refill.template after_step<2 * KT>(ks);
     chunk_end();
   }
@@ -360,7 +366,7 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
     if (ks >= KT / 2) {  // two of half 0's 2 DT = KT V^T fragments per chunk
 #pragma unroll
       for (int f = 2 * (ks - KT / 2); f < 2 * (ks - KT / 2) + 2; ++f)
-        va[f / DT][f % DT] = v_frag<D>(buf, 0, f / DT, f % DT, col, hh);
+        va[f / DT][f % DT] = fl.v(buf, 0, f / DT, f % DT);
     }
     refill.template after_step<2 * KT>(KT + ks);
     chunk_end();
@@ -371,7 +377,7 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
   for (int f = 0; f < 2 * DT; ++f) {
     const int c4 = f / DT, dt = f % DT;
     st.acc[dt] = mfma32x32x16(as_bf16x8(va[c4][dt]), h0.pb[c4], st.acc[dt]);
-    vb[c4][dt] = v_frag<D>(buf, 1, c4, dt, col, hh);
+    vb[c4][dt] = fl.v(buf, 1, c4, dt);
     h1.template part<2 * DT>(f, st, c);
     chunk_end();
   }
@@ -486,18 +492,35 @@ __device__ __forceinline__ void lds_barrier() {
 // matrix cores, the DMA of tiles i+1 .. i+R-1 is in flight.  One barrier per
 // tile: after it, tile i is visible to every wave and every wave has finished
 // tile i-1, whose slot then receives tile i+R-1 (or, past the last tile, tile
-// i again, read by nobody).  process(buf, id, refill) consumes tile i and
-// issues that refill's DMA rounds (between its score MFMAs, or all at once
-// when it has nothing to compute); the last tile goes to last(buf, id,
-// refill) instead, so that the loop body holds only the common case (an
-// exact stream's last tile may be a partial block).  `next()` yields tile ids
+// i again, read by nobody).  `runs` holds selected(id) and two consumers,
+// hit(buf, id, refill) for the wave's tiles and miss(buf, id, refill) for
+// the others; each consumes tile i and issues that refill's DMA rounds
+// (between its score MFMAs, or all at once when it has nothing to compute).
+// Consecutive tiles with the same selection run in an inner loop of their
+// own, so the accumulator is not split across a per-tile branch.  The last
+// tile goes to last(buf, id, refill) instead, so that the loop bodies hold
+// only the common case (an exact stream's last tile may be a partial
+// block).  `next()` yields tile ids
 // in order and is evaluated identically by every thread; source(id) is the
 // tile's HBM address.  R = 1: one slot, refilled after a barrier (latency
 // hidden by the other workgroups of the CU).  Two streams over the same ring
 // are separated by a barrier.
-template <int D, int NT, int R, typename Next, typename Source, typename Process, typename Last>
+// Selection predicate and the two tile consumers of a stream.
+template <typename Sel, typename Hit, typename Miss>
+struct TileRuns {
+  Sel selected;
+  Hit hit;
+  Miss miss;
+};
+
+template <typename Sel, typename Hit, typename Miss>
+__device__ __forceinline__ TileRuns<Sel, Hit, Miss> tile_runs(Sel selected, Hit hit, Miss miss) {
+  return {selected, hit, miss};
+}
+
+template <int D, int NT, int R, typename Next, typename Source, typename Runs, typename Last>
 __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next, Source source,
-                                            Process process, Last last, int wave, int lane) {
+                                            Runs runs, Last last, int wave, int lane) {
   using S = Shape<D>;
   constexpr int kRounds = S::TILE / 8 / NT;
   static_assert(R >= 1 && R <= 4 && (R & (R - 1)) == 0, "ring depth 1, 2 or 4");
@@ -511,8 +534,11 @@ __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next
       wait_vmcnt<0>();
       ring_barrier();
       if (i + 1 < count) {
-        if (process.selected(id)) process.hit(ring, id, NoRefill{});
-        else process.miss(ring, id, NoRefill{});
+        if (runs.selected(id)) {
+          runs.hit(ring, id, NoRefill{});
+        } else {
+          runs.miss(ring, id, NoRefill{});
+        }
       } else {
         last(ring, id, NoRefill{});
       }
@@ -542,16 +568,16 @@ __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next
   };
   int i = 0;
   while (i < count - 1) {
-    if (process.selected(ids[0])) {
+    if (runs.selected(ids[0])) {
       do {
-        step(i, process.hit);
+        step(i, runs.hit);
         ++i;
-      } while (i < count - 1 && process.selected(ids[0]));
+      } while (i < count - 1 && runs.selected(ids[0]));
     } else {
       do {
-        step(i, process.miss);
+        step(i, runs.miss);
         ++i;
-      } while (i < count - 1 && !process.selected(ids[0]));
+      } while (i < count - 1 && !runs.selected(ids[0]));
     }
   }
   step(count - 1, last);
@@ -779,10 +805,9 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
       centroid_tile<D>(st, buf, ct, approx, tk, qf, col, hh, scale_log2, refill);
     };
     auto always = [](int) { return true; };
-    struct { decltype(always) selected; decltype(process) hit; decltype(process) miss; } cruns{always, process, process};
     tile_stream<D, NT, R>(ring, nct, RangeCursor{0},
-                          [&](int ct) { return ctiles + int64_t(ct) * S::TILE; }, cruns, process,
-                          wave, lane);
+                          [&](int ct) { return ctiles + int64_t(ct) * S::TILE; },
+                          tile_runs(always, process, process), process, wave, lane);
     lds_barrier();  // every wave is done with the ring's centroid tiles
   }
   if (live && p.counts && lt == 0) {
@@ -797,13 +822,14 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
   const int count = cursor.count();
   const uint32_t* my_mask = s_mask[qg];
   const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
-  auto sel = [&](int j) { return ((my_mask[j >> 5] >> (j & 31)) & 1u) != 0; };
-  auto hit = [&](const uint16_t* buf, int j, const auto& refill) { full_tile<D>(st, buf, qf, col, hh, scale_log2, refill); };
-  auto miss = [&](const uint16_t* buf, int j, const auto& refill) { refill.all(); };
-  struct { decltype(sel) selected; decltype(hit) hit; decltype(miss) miss; } runs{sel, hit, miss};
+  auto selected = [&](int j) { return ((my_mask[j >> 5] >> (j & 31)) & 1u) != 0; };
+  auto hit = [&](const uint16_t* buf, int, const auto& refill) {
+    full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
+  };
+  auto miss = [&](const uint16_t*, int, const auto& refill) { refill.all(); };
   tile_stream<D, NT, R>(
       ring, count, cursor, [&](int j) { return tiles + int64_t(j) * S::TILE; },
-      runs,
+      tile_runs(selected, hit, miss),
       [&](const uint16_t* buf, int j, const auto& refill) {
         if ((my_mask[j >> 5] >> (j & 31)) & 1u) {
           exact_tile<D>(st, buf, j, tk, qf, col, hh, scale_log2, refill);
@@ -859,12 +885,11 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
   auto always = [](int) { return true; };
   auto hit = [&](const uint16_t* buf, int, const auto& refill) {
-        full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
-      };
-  struct { decltype(always) selected; decltype(hit) hit; decltype(hit) miss; } runs{always, hit, hit};
+    full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
+  };
   tile_stream<D, NT, 2>(
       ring, p.NKB, RangeCursor{0}, [&](int j) { return tiles + int64_t(j) * S::TILE; },
-      runs,
+      tile_runs(always, hit, hit),
       [&](const uint16_t* buf, int j, const auto& refill) {
         exact_tile<D>(st, buf, j, tk, qf, col, hh, scale_log2, refill);
       },

@@ -134,6 +134,17 @@ struct TileLayout {
   __device__ static __forceinline__ int vt_swizzle(int d) { return (d & 7) ^ ((d >> 3) & 1); }
   // Element offset of 16-byte fragment chunk c of feature row d.
   __device__ static __forceinline__ int vt_chunk(int d, int c) { return d * kBlock + 8 * (c ^ vt_swizzle(d)); }
+  // The MFMA operand reads as (lane part) + (XOR part ^ per-read constant):
+  // for key row r = 32 t + col and chunk c = 2 ks + hh,
+  //   k_offset(r, c) = r D + (k_lane_xor(col, hh) ^ 16 ks),
+  // and for feature row d = 32 dt + col and chunk c = 4 t + 2 c4 + hh,
+  //   vt_chunk(d, c) = d 64 + (vt_lane_xor(col, hh) ^ (32 t + 16 c4)),
+  // since the swizzles depend only on col and 2 ks, 4 t + 2 c4 leave bit 0 free.
+  __device__ static __forceinline__ int k_lane_xor(int col, int hh) {
+    const int sw = D == 128 ? (col & 15) : ((col >> 1) & 7);
+    return 8 * (hh ^ sw);
+  }
+  __device__ static __forceinline__ int vt_lane_xor(int col, int hh) { return 8 * (hh ^ vt_swizzle(col)); }
   // Element offset of 4-key group g (keys 4 g .. 4 g + 3) of feature row d.
   __device__ static __forceinline__ int vt_offset(int d, int g) {
     return vt_chunk(d, 2 * (g >> 2) + (g & 1)) + 4 * ((g >> 1) & 1);
