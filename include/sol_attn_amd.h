@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 2
+#define SOL_ABI_VERSION 3
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
 
@@ -60,8 +60,10 @@ const char* sol_last_error(void);
  *   sizes[3] key_mean    fp32 [batch, heads, head_dim]  (key_var has the same size)
  * Tile pairs: a K tile (64 rows x head_dim) then a V^T tile (head_dim rows x 64),
  * bank-swizzled: 16-byte chunk c of K row r at chunk c ^ (r & 15) (head_dim 128)
- * or c ^ ((r >> 1) & 7) (head_dim 64); 4-element group g of V^T row d at group
- * g ^ (d & 15) ^ ((d >> 4) & 1).  Rows past the last key / block are zero. */
+ * or c ^ ((r >> 1) & 7) (head_dim 64).  A V^T row is 8 chunks of 16 bytes;
+ * chunk c holds the 4-key groups 4 (c >> 1) + (c & 1) (low half) and that + 2
+ * (high half), and sits at chunk c ^ (d & 7) ^ ((d >> 3) & 1) of row d.
+ * Rows past the last key / block are zero. */
 int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
                    int64_t sizes[4]);
 
@@ -81,6 +83,28 @@ int sol_pool_kv(const void* k, const int64_t* k_strides,
                 float* chunk_sums, float* key_mean, float* key_var,
                 void* stream);
 
+/* Workspace bytes of sol_pair_strides (0: pairing does not apply, i.e. fewer
+ * than 4 or more than 8192 query blocks, or an unsupported shape).
+ * No counterpart in the reference (see sol_pair_strides). */
+int64_t sol_pair_workspace_size(int64_t batch, int64_t query_tokens, int64_t heads,
+                                int64_t head_dim);
+
+/* Query-block pairing for sol_attention_fwd.  Its workgroups hold two query
+ * blocks each and stream the union of their selected key blocks, so pairing
+ * blocks with similar selections shortens the stream.  Per (batch entry,
+ * head) this picks the stride s in 1..256 at which sol_attention_fwd pairs
+ * query blocks (block i with block i + s inside each run of 2 s blocks,
+ * adjacent pairs after the last full run): the one whose pairs have the most
+ * alike normalised query-block means (routing follows those means).  s = 1
+ * is the adjacent pairing.  Q and query_index as in sol_attention_fwd;
+ * workspace: sol_pair_workspace_size() bytes, 16-byte aligned; strides:
+ * int32 [batch, heads].  The pairing never changes results, only the
+ * schedule.  No counterpart in the reference (one Triton program per query
+ * block, no pairing). */
+int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* query_index,
+                     int64_t batch, int64_t query_tokens, int64_t heads, int64_t head_dim,
+                     void* workspace, int32_t* strides, void* stream);
+
 /* Fused routing + attention over the pooled keys of sol_pool_kv.
  * Replaces the `_threshold` and `_sol` launches of `launch_sol`
  * (kernels.py:203-225; kernels kernels.py:52-64 and 101-182).
@@ -88,6 +112,8 @@ int sol_pool_kv(const void* k, const int64_t* k_strides,
  * only); key_mean/key_var are read only for finite beta.  local_blocks < 0
  * disables the local band (indexed windows).  Sink token counts round
  * outward to whole blocks.  protection: NULL or uint8 [batch, NQB, NKB].
+ * pair_strides: NULL (adjacent query blocks share a workgroup) or int32
+ * [batch, heads] from sol_pair_strides (any value is a valid pairing).
  * out: contiguous BF16 [batch, query_tokens, heads, head_dim]; or, when
  * out_index (int64 [batch, query_tokens], device) is given, a contiguous BF16
  * [N, heads, head_dim] whose row out_index[b * query_tokens + t] receives
@@ -102,7 +128,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,
                       const void* tiles, const void* ctiles,
                       const float* key_mean, const float* key_var,
-                      const uint8_t* protection,
+                      const uint8_t* protection, const int32_t* pair_strides,
                       double scale, double beta, int64_t local_blocks,
                       int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,

@@ -17,7 +17,7 @@ import torch
 
 BLOCK = 64
 MAX_KEY_BLOCKS = 8192
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -34,8 +34,10 @@ _SIGNATURES = {
     "sol_pool_sizes": ([_i64, _i64, _i64, _i64, _i64p], ctypes.c_int),
     "sol_pool_kv": ([_p, _i64p, _p, _i64p, _p, _p, _i64, _i64, _i64, _i64,
                      _p, _p, _p, _p, _p, _p], ctypes.c_int),
+    "sol_pair_workspace_size": ([_i64, _i64, _i64, _i64], ctypes.c_int64),
+    "sol_pair_strides": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _p, _i64, _i64,
-                           _p, _p, _p, _p, _p,
+                           _p, _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
                            _p, _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
@@ -130,6 +132,29 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None):
             "key_blocks": nkb, "key_lengths": key_lengths}
 
 
+# Pair query blocks by the stride sol_pair_strides picks (False: adjacent
+# blocks share a workgroup).  Results are identical either way.
+PAIRING = True
+
+
+def pair_strides(q, rows=None):
+    """Per-(entry, head) query-block pairing strides (int32 ``[B, H]``), or None
+    when pairing does not apply (fewer than 4 or more than 8192 query blocks)."""
+    lib = library()
+    indexed = rows is not None
+    b, nq = rows.shape if indexed else q.shape[:2]
+    h, d = q.shape[-2:]
+    size = lib.sol_pair_workspace_size(b, nq, h, d)
+    if size == 0:
+        return None
+    q = _rows(q)
+    work = torch.empty(size // 4, device=q.device, dtype=torch.float32)
+    strides = torch.empty((b, h), device=q.device, dtype=torch.int32)
+    _check(lib.sol_pair_strides(_ptr(q), _strides(q, indexed), _ptr(rows), b, nq, h, d,
+                                _ptr(work), _ptr(strides), _stream(q.device)))
+    return strides
+
+
 def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows=None,
            debug=False, out=None):
     """Routing + attention over pooled keys (the ``_sol`` launch of ``kernels.py:218-224``).
@@ -167,11 +192,12 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     prot = None
     if protection is not None:
         prot = protection.contiguous().view(torch.uint8)
+    strides = pair_strides(q, rows) if PAIRING else None
     _check(lib.sol_attention_fwd(
         _ptr(q), _strides(q, indexed), _ptr(rows), b, nq, nk, _ptr(pooled.get("key_lengths")), h, d,
         _ptr(pooled["tiles"]), _ptr(pooled["ctiles"]),
         _ptr(pooled["mean"]), _ptr(pooled["var"]),
-        _ptr(prot), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
+        _ptr(prot), _ptr(strides), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
         _ptr(out), _ptr(rows if scatter else None), _ptr(counts),
         _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
         _stream(dev)))

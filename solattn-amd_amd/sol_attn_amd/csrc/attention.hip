@@ -651,10 +651,6 @@ __device__ __forceinline__ int slot_block(int s, int n, int stride) {
   return (s / run) * run + (w >> 1) + (w & 1) * stride;
 }
 
-#ifndef SOL_PAIR_STRIDE
-#define SOL_PAIR_STRIDE 0
-#endif
-
 // __launch_bounds__ second argument: minimum waves per SIMD.  Two waves per
 // SIMD leave each wave 256 VGPRs: the exact path keeps the 64-register
 // accumulator, 32 registers of Q fragments and 64 of K or V fragments live.
@@ -682,7 +678,9 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
   const int qg = wave >> 1, qh = wave & 1;  // query block in the group, query half
   const int lt = tid & 127;                  // thread index inside the query block's 2 waves
   const int qb0 = task.tile * G;  // first slot of this group
-  const int qb = slot_block(qb0 + qg, p.NQB, SOL_PAIR_STRIDE);
+  // Query-block pairing stride (any value is a valid pairing; see slot_block).
+  const int stride = p.pair_stride ? min(p.pair_stride[bh], p.NQB) : 0;
+  const int qb = slot_block(qb0 + qg, p.NQB, stride);
   const bool live = qb < p.NQB;
   const int tk = batch_tokens(p.klen, b, p.Tk);  // this entry's key tokens
   const int nkb = (tk + kBlock - 1) / kBlock;      // its key blocks (<= p.NKB, the buffer stride)
@@ -692,7 +690,7 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
   // 1. Q tiles -> LDS -> fragments.
   for (int idx = tid; idx < G * kBlock * S::DC; idx += NT) {
     const int r = idx / S::DC, c = idx % S::DC;
-    const int t = slot_block(qb0 + r / kBlock, p.NQB, SOL_PAIR_STRIDE) * kBlock + r % kBlock;
+    const int t = slot_block(qb0 + r / kBlock, p.NQB, stride) * kBlock + r % kBlock;
     const u32x4 x = t < p.Tq ? load16(p.q.row(b, t, h) + 8 * c) : zero_u32x4();
     *reinterpret_cast<u32x4*>(ring + r * S::KS + 8 * c) = x;
   }
@@ -754,7 +752,7 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
     for (int i = tid; i < G * nwords; i += NT) {
       const int g = i / nwords, w = i % nwords;
       const int nvalid = min(32, nkb - 32 * w);
-      s_mask[g][w] = slot_block(qb0 + g, p.NQB, SOL_PAIR_STRIDE) < p.NQB
+      s_mask[g][w] = slot_block(qb0 + g, p.NQB, stride) < p.NQB
                          ? (nvalid == 32 ? ~0u : ((1u << nvalid) - 1u)) : 0u;
     }
     if (live && p.dbg_selected)

@@ -128,11 +128,42 @@ int sol_pool_kv(const void* k, const int64_t* k_strides, const void* v, const in
                       stream);
 }
 
+int64_t sol_pair_workspace_size(int64_t batch, int64_t query_tokens, int64_t heads, int64_t head_dim) {
+  if (!shape_ok(batch, query_tokens, heads, head_dim)) return 0;
+  const int64_t nqb = cdiv(query_tokens, SOL_BLOCK);
+  if (nqb < 4 || nqb > sol::kMaxPairBlocks) return 0;
+  return batch * heads * head_dim * (nqb + sol::kMaxLag) * int64_t(sizeof(float));
+}
+
+int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* query_index,
+                     int64_t batch, int64_t query_tokens, int64_t heads, int64_t head_dim,
+                     void* workspace, int32_t* strides, void* stream) {
+  const int64_t bytes = sol_pair_workspace_size(batch, query_tokens, heads, head_dim);
+  if (bytes == 0)
+    return fail(SOL_ERR_UNSUPPORTED,
+                "sol_pair_strides: needs 4 .. 8192 query blocks and head_dim 64 or 128");
+  if (!operand_ok(q, q_strides, query_index != nullptr))
+    return fail(SOL_ERR_INVALID, "sol_pair_strides: Q needs 16-byte aligned rows and positive strides");
+  if (!workspace || !strides || !aligned16(workspace))
+    return fail(SOL_ERR_INVALID, "sol_pair_strides: workspace (16-byte aligned) and strides are required");
+  sol::PairParams p;
+  p.q = rows_of(q, q_strides, query_index, query_tokens);
+  p.B = int(batch);
+  p.H = int(heads);
+  p.Tq = int(query_tokens);
+  p.NQB = int(cdiv(query_tokens, SOL_BLOCK));
+  p.means = static_cast<float*>(workspace);
+  p.lags = p.means + batch * heads * head_dim * p.NQB;
+  p.strides = strides;
+  return hip_status(sol::launch_pairing(p, int(head_dim), static_cast<hipStream_t>(stream)));
+}
+
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,
                       const void* tiles, const void* ctiles, const float* key_mean,
-                      const float* key_var, const uint8_t* protection, double scale, double beta,
+                      const float* key_var, const uint8_t* protection,
+                      const int32_t* pair_strides, double scale, double beta,
                       int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
@@ -161,6 +192,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   sol::AttnParams p;
   std::memset(&p, 0, sizeof(p));
   p.q = rows_of(q, q_strides, query_index, query_tokens);
+  p.pair_stride = pair_strides;
   p.klen = key_lengths;
   p.out_index = out_index;
   p.tiles = static_cast<const uint16_t*>(tiles);

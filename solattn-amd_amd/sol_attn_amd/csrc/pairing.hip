@@ -1,0 +1,115 @@
+// Query-block pairing for the SOL attention workgroups.
+//
+// A SOL workgroup holds two query blocks and streams the union of their
+// selected key blocks, so its time follows the union while its useful work
+// follows the sum: pairing query blocks whose selections overlap shortens the
+// stream.  A query block's selection is a function of its mean (the routing
+// proxy is q_mean . k_mean, tested against a cutoff built from the same
+// q_mean), so the pairing is chosen from the query-block means before any
+// routing, per (batch entry, head):
+//   1. m_i = mean of query block i, normalised to unit length;
+//   2. c(s) = mean over i of m_i . m_{i+s} for every lag s = 1 .. kMaxLag;
+//   3. the stride s maximising the mean cosine of the pairs the attention
+//      kernel would form at that stride -- (i, i+s) inside each full run of
+//      2 s blocks, adjacent pairs after the last full run:
+//        score(s) = (covered(s) c(s) + (NQB - covered(s)) c(1)) / NQB.
+// Lag s = 1 is the adjacent pairing.  For a video latent laid out frame by
+// frame with W blocks per frame this finds s = W (the same spatial block in
+// the next frame).  Pairing changes which blocks share a workgroup, never a
+// block's own computation: outputs are identical for every stride.
+// The reference runs one Triton program per query block and has no
+// counterpart.
+#include "sol_device.h"
+#include "sol_internal.h"
+
+namespace sol {
+
+namespace {
+
+// Normalised query-block means: m[((b H + h) D + d) NQB + i] (lag-major rows
+// so that the lag kernel reads one feature of one head contiguously).
+template <int D>
+__global__ __launch_bounds__(256) void qblock_means_kernel(PairParams p) {
+  constexpr int DC = D / 8;  // 16-byte chunks per row = threads per head
+  const int qb = blockIdx.x, b = blockIdx.y;
+  const int qlen = min(kBlock, p.Tq - qb * kBlock);
+  const int chunks = p.H * DC;
+  for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
+    const int h = c / DC, dc = c % DC;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int r = 0; r < qlen; ++r) {
+      const u32x4 x = load16(p.q.row(b, qb * kBlock + r, h) + 8 * dc);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w = x[e >> 1];
+        s[e] += bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu));
+      }
+    }
+    float n2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[e] /= float(qlen);
+      n2 += s[e] * s[e];
+    }
+    // The DC threads of one head are consecutive lanes of one wave (chunk
+    // groups start at multiples of DC, and DC divides the wave width).
+#pragma unroll
+    for (int off = 1; off < DC; off <<= 1) n2 += __shfl_xor(n2, off);
+    const float inv = n2 > 0.f ? rsqrtf(n2) : 0.f;
+    float* dst = p.means + ((int64_t(b) * p.H + h) * D + 8 * dc) * p.NQB + qb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[int64_t(e) * p.NQB] = s[e] * inv;
+  }
+}
+
+// Lag sums of one feature d of one (batch entry, head): thread t holds lag
+// s = t + 1, sum over i of m_i[d] m_{i+s}[d].
+__global__ __launch_bounds__(kMaxLag) void pair_lag_kernel(PairParams p, int D) {
+  __shared__ float x[kMaxPairBlocks];
+  const int d = blockIdx.x, bh = blockIdx.y;
+  const float* src = p.means + (int64_t(bh) * D + d) * p.NQB;
+  for (int i = threadIdx.x; i < p.NQB; i += blockDim.x) x[i] = src[i];
+  __syncthreads();
+  const int s = threadIdx.x + 1;
+  float acc = 0.f;
+  for (int i = 0; i + s < p.NQB; ++i) acc = fmaf(x[i], x[i + s], acc);
+  p.lags[(int64_t(bh) * D + d) * kMaxLag + threadIdx.x] = acc;
+}
+
+// Per (batch entry, head): mean cosine per lag, pairing score per stride,
+// argmax (the smallest stride on ties).
+__global__ __launch_bounds__(kMaxLag) void pair_pick_kernel(PairParams p, int D) {
+  __shared__ float s_score[kMaxLag];
+  __shared__ float s_c1;
+  const int bh = blockIdx.x, t = threadIdx.x, s = t + 1;
+  const int n = p.NQB;
+  float r = 0.f;
+  for (int d = 0; d < D; ++d) r += p.lags[(int64_t(bh) * D + d) * kMaxLag + t];
+  const float c = n - s > 0 ? r / float(n - s) : 0.f;  // mean cosine at lag s
+  if (t == 0) s_c1 = c;
+  __syncthreads();
+  const int covered = (n / (2 * s)) * (2 * s);  // blocks that a stride-s pairing pairs at lag s
+  s_score[t] = covered > 0 ? (float(covered) * c + float(n - covered) * s_c1) / float(n) : -2.f;
+  __syncthreads();
+  if (t == 0) {
+    int best = 0;
+    for (int i = 1; i < kMaxLag; ++i)
+      if (s_score[i] > s_score[best]) best = i;
+    p.strides[bh] = best + 1;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream) {
+  if (D == 128)
+    hipLaunchKernelGGL(qblock_means_kernel<128>, dim3(p.NQB, p.B), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(qblock_means_kernel<64>, dim3(p.NQB, p.B), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL(pair_lag_kernel, dim3(D, p.B * p.H), dim3(kMaxLag), 0, stream, p, D);
+  hipLaunchKernelGGL(pair_pick_kernel, dim3(p.B * p.H), dim3(kMaxLag), 0, stream, p, D);
+  return hipGetLastError();
+}
+
+}  // namespace sol

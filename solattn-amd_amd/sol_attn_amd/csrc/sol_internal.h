@@ -28,8 +28,21 @@ struct PoolParams {
                                  // (NKB, NCT: for Tk; ragged entries use a prefix)
 };
 
+// Query-block pairing (pairing.hip).
+constexpr int kMaxLag = 256;           // strides considered: 1 .. kMaxLag
+constexpr int kMaxPairBlocks = 8192;   // query blocks per (entry, head) the lag kernel holds in LDS
+
+struct PairParams {
+  TokenRows q;
+  float* means;      // [B, H, D, NQB] normalised query-block means
+  float* lags;       // [B, H, D, kMaxLag] per-feature lag sums
+  int32_t* strides;  // [B, H] chosen pairing stride
+  int B, H, Tq, NQB;
+};
+
 struct AttnParams {
   TokenRows q;
+  const int32_t* pair_stride;  // [B, H] query-block pairing stride, or null: adjacent pairs
   const int32_t* klen;         // [B] key tokens per batch entry (<= Tk), or null: all Tk
   const int64_t* out_index;    // [B, Tq] output rows of an [N, H, D] output, or null
   const uint16_t* tiles;       // [B, H, NKB, 2, 64 * D] from the pooling pass
@@ -52,5 +65,6 @@ struct AttnParams {
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream);
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_dense(const AttnParams& p, int D, hipStream_t stream);
+hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream);
 
 }  // namespace sol

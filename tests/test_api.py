@@ -113,7 +113,7 @@ def test_stats_density():
 
 def _declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(sol_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int64_t|int|const char\*)\s+(sol_\w+)\(", text, re.M)))
 
 
 def test_c_abi_library_exports_every_declared_symbol():
@@ -127,13 +127,17 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == 2
+    assert native.sol_abi_version() == 3
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
     assert list(sizes) == [1 * 2 * 1 * tile, 1 * 2 * 5 * tile, 1 * 2 * 1 * 2 * 64 * 4, 2 * 64 * 4]
     assert native.sol_pool_sizes(1, 317, 2, 96, sizes) == -1
     assert b"invalid shape" in native.sol_last_error()
+    # Pairing workspace: [B, H, D, NQB + 256] fp32; none below 4 query blocks.
+    assert native.sol_pair_workspace_size(1, 193, 2, 64) == 2 * 64 * (4 + 256) * 4
+    assert native.sol_pair_workspace_size(1, 192, 2, 64) == 0
+    assert native.sol_pair_workspace_size(1, 193, 2, 96) == 0
 
 
 def test_c_abi_rejects_bad_arguments_without_launching():
@@ -146,9 +150,13 @@ def test_c_abi_rejects_bad_arguments_without_launching():
                               float("nan"), fake, fake, None)
     assert rc == -1 and b"scale" in native.sol_last_error()
     rc = native.sol_attention_fwd(fake, strides, None, 1, 193, 317, None, 2, 64, fake, fake,
-                                  None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None,
-                                  None, None, None)
+                                  None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None,
+                                  None, None, None, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
+    rc = native.sol_pair_strides(fake, strides, None, 1, 192, 2, 64, fake, fake, None)
+    assert rc == -2 and b"4 .. 8192 query blocks" in native.sol_last_error()
+    rc = native.sol_pair_strides(fake, strides, None, 1, 193, 2, 64, None, fake, None)
+    assert rc == -1 and b"workspace" in native.sol_last_error()
     bad = (ctypes.c_int64 * 3)(64 * 2 * 317, 127, 64)
     rc = native.sol_pool_kv(fake, bad, fake, strides, None, None, 1, 317, 2, 64, fake, fake,
                             None, None, None, None)
