@@ -26,25 +26,32 @@ namespace sol {
 
 namespace {
 
+constexpr int kMeanThreads = 512;  // one 16-byte chunk per thread for up to 32 heads of 128
+
 // Normalised query-block means: m[((b H + h) D + d) NQB + i] (lag-major rows
 // so that the lag kernel reads one feature of one head contiguously).
 template <int D>
-__global__ __launch_bounds__(256) void qblock_means_kernel(PairParams p) {
+__global__ __launch_bounds__(kMeanThreads) void qblock_means_kernel(PairParams p) {
   constexpr int DC = D / 8;  // 16-byte chunks per row = threads per head
+  constexpr int kRows = 16;  // row loads in flight per thread
   const int qb = blockIdx.x, b = blockIdx.y;
   const int qlen = min(kBlock, p.Tq - qb * kBlock);
   const int chunks = p.H * DC;
   for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
     const int h = c / DC, dc = c % DC;
     float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int r = 0; r < qlen; ++r) {
-      const u32x4 x = load16(p.q.row(b, qb * kBlock + r, h) + 8 * dc);
+    for (int r0 = 0; r0 < qlen; r0 += kRows) {
+      u32x4 x[kRows];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t w = x[e >> 1];
-        s[e] += bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu));
-      }
+      for (int r = 0; r < kRows; ++r)
+        x[r] = r0 + r < qlen ? load16(p.q.row(b, qb * kBlock + r0 + r, h) + 8 * dc) : zero_u32x4();
+#pragma unroll
+      for (int r = 0; r < kRows; ++r)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t w = x[r][e >> 1];
+          s[e] += bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu));
+        }
     }
     float n2 = 0.f;
 #pragma unroll
@@ -72,9 +79,13 @@ __global__ __launch_bounds__(kMaxLag) void pair_lag_kernel(PairParams p, int D) 
   for (int i = threadIdx.x; i < p.NQB; i += blockDim.x) x[i] = src[i];
   __syncthreads();
   const int s = threadIdx.x + 1;
-  float acc = 0.f;
-  for (int i = 0; i + s < p.NQB; ++i) acc = fmaf(x[i], x[i + s], acc);
-  p.lags[(int64_t(bh) * D + d) * kMaxLag + threadIdx.x] = acc;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // independent chains
+  int i = 0;
+  for (; i + 3 + s < p.NQB; i += 4)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] = fmaf(x[i + u], x[i + u + s], acc[u]);
+  for (; i + s < p.NQB; ++i) acc[0] = fmaf(x[i], x[i + s], acc[0]);
+  p.lags[(int64_t(bh) * D + d) * kMaxLag + threadIdx.x] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
 }
 
 // Per (batch entry, head): mean cosine per lag, pairing score per stride,
@@ -84,8 +95,11 @@ __global__ __launch_bounds__(kMaxLag) void pair_pick_kernel(PairParams p, int D)
   __shared__ float s_c1;
   const int bh = blockIdx.x, t = threadIdx.x, s = t + 1;
   const int n = p.NQB;
-  float r = 0.f;
-  for (int d = 0; d < D; ++d) r += p.lags[(int64_t(bh) * D + d) * kMaxLag + t];
+  float part[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // loads in flight
+  for (int d = 0; d < D; d += 8)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) part[u] += p.lags[(int64_t(bh) * D + d + u) * kMaxLag + t];
+  const float r = ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
   const float c = n - s > 0 ? r / float(n - s) : 0.f;  // mean cosine at lag s
   if (t == 0) s_c1 = c;
   __syncthreads();
@@ -104,9 +118,9 @@ __global__ __launch_bounds__(kMaxLag) void pair_pick_kernel(PairParams p, int D)
 
 hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream) {
   if (D == 128)
-    hipLaunchKernelGGL(qblock_means_kernel<128>, dim3(p.NQB, p.B), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(qblock_means_kernel<128>, dim3(p.NQB, p.B), dim3(kMeanThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL(qblock_means_kernel<64>, dim3(p.NQB, p.B), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(qblock_means_kernel<64>, dim3(p.NQB, p.B), dim3(kMeanThreads), 0, stream, p);
   hipLaunchKernelGGL(pair_lag_kernel, dim3(D, p.B * p.H), dim3(kMaxLag), 0, stream, p, D);
   hipLaunchKernelGGL(pair_pick_kernel, dim3(p.B * p.H), dim3(kMaxLag), 0, stream, p, D);
   return hipGetLastError();
