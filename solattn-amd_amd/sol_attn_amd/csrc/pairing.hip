@@ -42,9 +42,7 @@ __global__ __launch_bounds__(kMeanThreads) void qblock_means_kernel(PairParams p
     float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int r0 = 0; r0 < qlen; r0 += kRows) {
       u32x4 x[kRows];
-#pragma unroll
-      for (int r = 0; r < kRows; ++r)
-        x[r] = r0 + r < qlen ? load16(p.q.row(b, qb * kBlock + r0 + r, h) + 8 * dc) : zero_u32x4();
+      load_rows16(p.q, b, qb * kBlock + r0, qb * kBlock + qlen - 1, h, 8 * dc, x);
 #pragma unroll
       for (int r = 0; r < kRows; ++r)
 #pragma unroll

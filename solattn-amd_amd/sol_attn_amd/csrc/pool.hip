@@ -21,8 +21,12 @@
 
 namespace sol {
 
+// One wave per SIMD: each wave keeps 16 rows x 16 bytes per lane in flight,
+// so one workgroup per CU already has ~16 MB of reads outstanding chip-wide.
+// More waves only deepen the memory queues: the pass measured 0.50 ms at 3
+// waves per SIMD, 0.47 ms at 2 and 0.42 ms at 1 (same code otherwise).
 template <int D>
-__global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void pool_kv_kernel(PoolParams p) {
   constexpr int DC = D / 8;          // 16-byte chunks per token row
   constexpr int LPB = DC * 4;        // lanes per key block: 4 chunks of 16 rows
   constexpr int BPI = kWave / LPB;   // key blocks per wave iteration
@@ -31,8 +35,11 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
 
   const bool is_v = blockIdx.y != 0;
   const TokenRows src = is_v ? p.v : p.k;
-  const int c = blockIdx.x % p.NCHP;
-  const int bh = blockIdx.x / p.NCHP;
+  // Heads vary fastest over the grid: the workgroups in flight together read
+  // whole token rows (all heads of the same tokens), so the DRAM pages they
+  // open are read through instead of in 2 D-byte pieces far apart in time.
+  const int c = blockIdx.x / (p.B * p.H);
+  const int bh = blockIdx.x % (p.B * p.H);
   const int h = bh % p.H, b = bh / p.H;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int sub = lane / LPB, r4 = (lane % LPB) / DC, dc = lane % DC;
@@ -50,11 +57,7 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
     if (j < nkb) {
       len = min(kBlock, tk - kBlock * j);
       u32x4 x[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int t = 16 * r4 + i;
-        x[i] = t < len ? load16(src.row(b, kBlock * j + t, h) + 8 * dc) : zero_u32x4();
-      }
+      load_rows16(src, b, kBlock * j + 16 * r4, kBlock * j + len - 1, h, 8 * dc, x);
       if (p.tiles) {
         // Attention-ready tiles: K rows as loaded, V transposed 8x8 in registers.
         uint16_t* tile = p.tiles + ((int64_t(b) * p.H + h) * p.NKB + j) * 2 * TL::kElems;
@@ -63,20 +66,21 @@ __global__ __launch_bounds__(256) void pool_kv_kernel(PoolParams p) {
           for (int i = 0; i < 16; ++i)
             *reinterpret_cast<u32x4*>(tile + TL::k_offset(16 * r4 + i, dc)) = x[i];
         } else {
+          // A Vᵀ chunk holds 4-key groups g and g + 2 of one feature, so the
+          // 8x8 transpose takes rows 16 r4 + 4 sb + {0..3, 8..11}: each
+          // transposed row is then one whole 16-byte chunk (group 4 r4 + sb
+          // in its low half, 4 r4 + sb + 2 in its high half).
           uint16_t* vt = tile + TL::kElems;
 #pragma unroll
           for (int sb = 0; sb < 2; ++sb) {
             u32x4 rows[8], cols[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) rows[i] = x[8 * sb + i];
+            for (int i = 0; i < 8; ++i) rows[i] = x[4 * sb + (i < 4 ? i : i + 4)];
             transpose8x8(rows, cols);
-            const int g0 = 4 * r4 + 2 * sb;  // 4-key group of keys 16 r4 + 8 sb
+            const int g = 4 * r4 + sb;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int d = 8 * dc + e;
-              *reinterpret_cast<u32x2*>(vt + TL::vt_offset(d, g0)) = u32x2{cols[e][0], cols[e][1]};
-              *reinterpret_cast<u32x2*>(vt + TL::vt_offset(d, g0 + 1)) = u32x2{cols[e][2], cols[e][3]};
-            }
+            for (int e = 0; e < 8; ++e)
+              *reinterpret_cast<u32x4*>(vt + TL::vt_offset(8 * dc + e, g)) = cols[e];
           }
         }
       }

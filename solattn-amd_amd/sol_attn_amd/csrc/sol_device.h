@@ -83,8 +83,42 @@ struct TokenRows {
   }
 };
 
+// Operand rows live in global memory: loads through a global-space pointer
+// are global_load (vector memory counter only), not flat loads that also
+// count against the LDS counter.
+typedef const u32x4 __attribute__((address_space(1)))* global_u32x4_ptr;
+
 __device__ __forceinline__ u32x4 load16(const uint16_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
+  return *(global_u32x4_ptr)(p);
+}
+
+// 16 bytes at element offset `col` of rows t0 .. t0 + N - 1 of entry b, head
+// h; rows past t_last (a valid row) read as zero.  The addresses are formed
+// first (the index entries of an indexed source all in flight together) and
+// every data load is then issued unconditionally -- rows past t_last re-read
+// row t_last -- so the N loads are in flight at once instead of each waiting
+// behind a branch.
+template <int N>
+__device__ __forceinline__ void load_rows16(const TokenRows& r, int b, int t0, int t_last, int h, int col,
+                                            u32x4 (&x)[N]) {
+  const uint16_t* p[N];
+  if (r.index) {
+    const int64_t* idx = r.index + int64_t(b) * r.T;
+    int64_t row[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) row[i] = idx[min(t0 + i, t_last)];
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = r.base + row[i] * r.st + int64_t(h) * r.sh + col;
+  } else {
+    const uint16_t* base = r.base + int64_t(b) * r.sb + int64_t(h) * r.sh + col;
+#pragma unroll
+    for (int i = 0; i < N; ++i) p[i] = base + int64_t(min(t0 + i, t_last)) * r.st;
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) x[i] = load16(p[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    if (t0 + i > t_last) x[i] = zero_u32x4();
 }
 
 __device__ __forceinline__ u32x2 load8(const uint16_t* p) {
