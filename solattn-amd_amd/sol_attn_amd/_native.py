@@ -135,17 +135,25 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None):
 # Pair query blocks by the stride sol_pair_strides picks (False: adjacent
 # blocks share a workgroup).  Results are identical either way.
 PAIRING = True
+# Launches with fewer query blocks over all (entry, head) pairs are not
+# paired: the three pairing kernels cost ~27 us, more than the union they
+# save on a short attention launch.
+PAIR_MIN_QUERY_BLOCKS = 8192
 
 
-def pair_strides(q, rows=None):
+def pair_strides(q, rows=None, min_blocks=None):
     """Per-(entry, head) query-block pairing strides (int32 ``[B, H]``), or None
-    when pairing does not apply (fewer than 4 or more than 8192 query blocks)."""
+    when pairing does not apply: fewer than ``min_blocks`` query blocks in
+    all (by default PAIR_MIN_QUERY_BLOCKS), or a sequence outside the
+    library's 4 .. 8192 query blocks."""
     lib = library()
     indexed = rows is not None
     b, nq = rows.shape if indexed else q.shape[:2]
     h, d = q.shape[-2:]
     size = lib.sol_pair_workspace_size(b, nq, h, d)
-    if size == 0:
+    if min_blocks is None:
+        min_blocks = PAIR_MIN_QUERY_BLOCKS
+    if size == 0 or b * h * -(-nq // BLOCK) < min_blocks:
         return None
     q = _rows(q)
     work = torch.empty(size // 4, device=q.device, dtype=torch.float32)

@@ -54,7 +54,7 @@ def pairing_scores(q):
 
 def test_chosen_stride_is_the_frame_period():
     q = frames(12, 7).cuda()
-    strides = _native.pair_strides(q)
+    strides = _native.pair_strides(q, min_blocks=4)
     assert strides.shape == (1, 2) and strides.dtype == torch.int32
     assert strides.cpu().tolist() == [[7, 7]]
 
@@ -62,18 +62,20 @@ def test_chosen_stride_is_the_frame_period():
 @pytest.mark.parametrize("seed", [1, 2])
 def test_chosen_stride_maximises_the_score(seed):
     q = frames(9, 11, heads=3, d=64, seed=seed, noise=1.5)
-    got = _native.pair_strides(q.cuda()).cpu().numpy()[0]
+    got = _native.pair_strides(q.cuda(), min_blocks=4).cpu().numpy()[0]
     scores = pairing_scores(q[0])
     for h in range(3):
         assert scores[h, got[h] - 1] >= scores[h].max() - 1e-5, (h, got[h], scores[h].argmax() + 1)
 
 
 def test_no_pairing_below_four_query_blocks():
-    assert _native.pair_strides(frames(1, 3).cuda()) is None
+    assert _native.pair_strides(frames(1, 3).cuda(), min_blocks=1) is None
+    assert _native.pair_strides(frames(12, 7).cuda()) is None  # below the default minimum
 
 
 @pytest.mark.parametrize("beta", [1.0, -math.inf, 0.0])
 def test_pairing_never_changes_results(beta, monkeypatch):
+    monkeypatch.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)  # pair these 72 query blocks
     q, k, v = (frames(8, 9, seed=s).cuda() for s in (3, 4, 5))
     ref, ref_stats = sol_attention(q, k, v, beta=beta, kv_sink_tokens=64, return_stats=True)
     monkeypatch.setattr(_native, "PAIRING", False)
@@ -83,7 +85,7 @@ def test_pairing_never_changes_results(beta, monkeypatch):
     # Forced strides (including ones past the query blocks) are valid pairings too.
     pooled = _native.pool_kv(k, v, moments=not math.isinf(beta))
     for s in (1, 2, 5, 9, 40, 1 << 30):
-        monkeypatch.setattr(_native, "pair_strides", lambda q, rows=None, s=s: torch.full(
+        monkeypatch.setattr(_native, "pair_strides", lambda q, rows=None, s=s, **kw: torch.full(
             (1, 2), s, device=q.device, dtype=torch.int32))
         monkeypatch.setattr(_native, "PAIRING", True)
         out, counts, _ = _native.attend(q, pooled, 128 ** -0.5, beta, 1, 64, 0)
@@ -92,12 +94,13 @@ def test_pairing_never_changes_results(beta, monkeypatch):
 
 
 def test_indexed_windows_pair_per_window(monkeypatch):
+    monkeypatch.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)
     x = [frames(10, 6, seed=s)[0].cuda() for s in (6, 7, 8)]      # [T, H, D] NHD
     t = x[0].shape[0]
     rows = torch.stack((torch.arange(0, t // 2), torch.arange(t // 2, t)))
     keys = torch.stack((torch.arange(0, t - 64), torch.arange(64, t)))
     plan = IndexedPlan.create(rows, keys, t, protected_ranges=((0, 64),), local_tokens=64).to("cuda")
-    strides = _native.pair_strides(x[0], plan.rows)
+    strides = _native.pair_strides(x[0], plan.rows, min_blocks=4)
     assert strides.shape == (2, 2)
     ref = sol_attention_indexed(*x, plan, beta=1.0)
     monkeypatch.setattr(_native, "PAIRING", False)
