@@ -432,17 +432,28 @@ __device__ __forceinline__ void centroid_tile(State<D>& st, const uint16_t* buf,
                                               int tk, const bf16x8 (&qf)[Shape<D>::KT], int col, int hh,
                                               float c, const Refill& refill) {
   const uint64_t lane_approx = approx >> (4 * hh);
-  const int lane_tokens = fresh(tk - kBlock * (kBlock * ct + 4 * hh));  // keys from the lane's first block on
   const float inv_c = 1.f / c;
+  // Every block of the tile is whole unless it holds the sequence's partial
+  // last block; whole blocks share one offset, log2(64) / c, computed as the
+  // per-block formula computes it at len 64.
+  const bool whole_tile = kBlock * kBlock * (ct + 1) <= tk;
+  const float whole = __builtin_amdgcn_logf(float(kBlock)) * inv_c;
+  const int lane_tokens = tk - kBlock * (kBlock * ct + 4 * hh);  // keys from the lane's first block on
   tile_attend<D, true>(st, buf, qf, col, hh, c,
                        [&](int t) {
                          f32x16 bias;
+                         if (whole_tile) {
 #pragma unroll
-                         for (int e = 0; e < 16; ++e) {
-                           const int row = tile_row(t, e, 0);
-                           const int len = min(kBlock, lane_tokens - kBlock * row);
-                           bias[e] = ((lane_approx >> row) & 1u)
-                                         ? __builtin_amdgcn_logf(float(len)) * inv_c : kNegInf;
+                           for (int e = 0; e < 16; ++e)
+                             bias[e] = ((lane_approx >> tile_row(t, e, 0)) & 1u) ? whole : kNegInf;
+                         } else {
+#pragma unroll
+                           for (int e = 0; e < 16; ++e) {
+                             const int row = tile_row(t, e, 0);
+                             const int len = min(kBlock, lane_tokens - kBlock * row);
+                             bias[e] = ((lane_approx >> row) & 1u)
+                                           ? __builtin_amdgcn_logf(float(len)) * inv_c : kNegInf;
+                           }
                          }
                          return bias;
                        },
