@@ -511,9 +511,10 @@ __device__ __forceinline__ void lds_barrier() {
 // own, so the accumulator is not split across a per-tile branch.  The last
 // tile goes to last(buf, id, refill) instead, so that the loop bodies hold
 // only the common case (an exact stream's last tile may be a partial
-// block).  `next()` yields tile ids
-// in order and is evaluated identically by every thread; source(id) is the
-// tile's HBM address.  R = 1: one slot, refilled after a barrier (latency
+// block).  `next()` yields tile references (ids, or tags that carry an
+// id) in order; the tile each reference names is the same for every thread,
+// while selected(ref) may differ between waves.  source(ref) is the tile's
+// HBM address.  R = 1: one slot, refilled after a barrier (latency
 // hidden by the other workgroups of the CU).  Two streams over the same ring
 // are separated by a barrier.
 // Selection predicate and the two tile consumers of a stream.
@@ -607,15 +608,19 @@ __device__ __forceinline__ uint64_t tile_approx(const uint32_t* mask, int ct, in
 }
 
 // Exact tiles of a SOL workgroup: the union of its G query blocks' selected
-// blocks, ascending.  The exact phase starts (word 0 loaded) on the first
-// call; the word scan never passes the last mask word and every id is below
-// nkb, so the cursor yields valid tiles even if called more than count() times.
+// blocks, ascending, as tags 2 j + (whether the calling wave's own query
+// block selected j), so that the stream needs no LDS read per tile to tell
+// the wave's tiles from its partners'.  The exact phase starts (word 0
+// loaded) on the first call; the word scan never passes the last mask word
+// and every id is below nkb, so the cursor yields valid tiles even if called
+// more than count() times.
 template <int G>
 struct UnionCursor {
   const uint32_t* mask;  // [G][stride] routing bitmasks
+  const uint32_t* mine;  // the calling wave's own row of mask
   int stride, nkb;
   int word = -1;
-  uint32_t bits = 0u;
+  uint32_t bits = 0u, own = 0u;
 
   __device__ __forceinline__ uint32_t union_word(int w) const {
     uint32_t u = 0;
@@ -628,17 +633,20 @@ struct UnionCursor {
     for (int w = 0; w < (nkb + 31) / 32; ++w) n += __builtin_popcount(union_word(w));
     return n;
   }
+  __device__ __forceinline__ void load(int w) {
+    word = w;
+    bits = union_word(w);
+    own = uint32_t(__builtin_amdgcn_readfirstlane(mine[w]));  // wave-uniform: the wave's own row
+  }
   __device__ __forceinline__ int operator()() {
     const int last = (nkb + 31) / 32 - 1;
-    if (word < 0) {
-      word = 0;
-      bits = union_word(0);
-    }
-    while (bits == 0 && word < last) bits = union_word(++word);
+    if (word < 0) load(0);
+    while (bits == 0 && word < last) load(word + 1);
     if (bits == 0) return 0;  // unreachable when called count() times
-    const int j = word * 32 + __builtin_ctz(bits);
+    const int b = __builtin_ctz(bits);
+    const int j = word * 32 + b;
     bits &= bits - 1u;
-    return j < nkb ? j : 0;
+    return j < nkb ? 2 * j + int((own >> b) & 1u) : 0;
   }
 };
 
@@ -827,21 +835,21 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
 
   // 4. Exact pass over the union of the group's selected blocks.  Only the
   // stream's last tile can be the partial tail block.
-  UnionCursor<G> cursor{&s_mask[0][0], kMaskWords, nkb};
+  // Tile ids travel as tags 2 j + own-selection bit (UnionCursor).
+  UnionCursor<G> cursor{&s_mask[0][0], s_mask[qg], kMaskWords, nkb};
   const int count = cursor.count();
-  const uint32_t* my_mask = s_mask[qg];
   const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
-  auto selected = [&](int j) { return ((my_mask[j >> 5] >> (j & 31)) & 1u) != 0; };
+  auto selected = [](int tag) { return (tag & 1) != 0; };
   auto hit = [&](const uint16_t* buf, int, const auto& refill) {
     full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
   };
   auto miss = [&](const uint16_t*, int, const auto& refill) { refill.all(); };
   tile_stream<D, NT, R>(
-      ring, count, cursor, [&](int j) { return tiles + int64_t(j) * S::TILE; },
+      ring, count, cursor, [&](int tag) { return tiles + int64_t(tag >> 1) * S::TILE; },
       tile_runs(selected, hit, miss),
-      [&](const uint16_t* buf, int j, const auto& refill) {
-        if ((my_mask[j >> 5] >> (j & 31)) & 1u) {
-          exact_tile<D>(st, buf, j, tk, qf, col, hh, scale_log2, refill);
+      [&](const uint16_t* buf, int tag, const auto& refill) {
+        if (tag & 1) {
+          exact_tile<D>(st, buf, tag >> 1, tk, qf, col, hh, scale_log2, refill);
         } else {
           refill.all();
         }
