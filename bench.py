@@ -127,6 +127,15 @@ def bench_windows(q, k, v, cfg, reps, check_cpu):
     plan_dev = plan.to(q.device)
     torch.cuda.synchronize()
     t_setup = time.perf_counter() - t0
+    # The same plan built on the GPU from device-resident indices.
+    rows_dev, keys_dev = rows.to(q.device), [x.to(q.device) for x in keys]
+    IndexedPlan.create(rows_dev, keys_dev, n, **prot)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    plan_gpu = IndexedPlan.create(rows_dev, keys_dev, n, **prot)
+    torch.cuda.synchronize()
+    t_gpu = time.perf_counter() - t0
+    gpu_plan_equal = bool(torch.equal(plan_gpu.protected_blocks, plan_dev.protected_blocks))
     groups = {}
     for w, kv in enumerate(keys):
         groups.setdefault(len(kv), []).append(w)
@@ -156,7 +165,8 @@ def bench_windows(q, k, v, cfg, reps, check_cpu):
            "plans": len(groups), "speedup_one_call": per_ms / ragged_ms,
            "dense_equiv_tflops": flops / (ragged_ms * 1e-3) / 1e12, "dense_equiv_flops": flops,
            "density": stats.density(), "identical_to_per_plan_route": agree,
-           "plan_create_s": t_create, "plan_setup_s": t_setup}
+           "plan_create_s": t_create, "plan_setup_s": t_setup,
+           "plan_create_gpu_s": t_gpu, "gpu_plan_identical": gpu_plan_equal}
     if check_cpu:
         from oracle import sol_oracle as orc
         w = cfg["frames"] // 2

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 3
+#define SOL_ABI_VERSION 4
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
 
@@ -134,6 +134,23 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
                       void* stream);
+
+/* Packed-block protection of indexed windows, built on the GPU: the
+ * protection part of `IndexedPlan.create` (indexed.py:27-62).  Block (w, qb,
+ * kb) of protected_blocks (uint8 [windows, NQB, NKB]) is 1 when one of the
+ * window's keys at positions 64 kb .. 64 kb + 63 (and below its key count)
+ * has an original index inside [rows[w, 64 qb] - local_tokens,
+ * rows[w, last row of qb] + local_tokens] or inside a protected range.
+ * rows: int64 [windows, query_rows]; keys: int64 [windows, key_count]; both
+ * strictly increasing per window (over a window's first key_lengths[w] keys
+ * when key_lengths, int32 [windows], is given; later positions are never
+ * read).  ranges: int64 [nranges, 2] ranges [a, b), NULL when nranges is 0.
+ * All pointers are device memory.  Indices are not validated here: the
+ * Python layer checks them first, as `IndexedPlan.create` does. */
+int sol_plan_protection(const int64_t* rows, const int64_t* keys, const int32_t* key_lengths,
+                        int64_t windows, int64_t query_rows, int64_t key_count,
+                        int64_t local_tokens, const int64_t* ranges, int64_t nranges,
+                        uint8_t* protected_blocks, void* stream);
 
 /* Non-causal BF16 attention over all keys, FP32 softmax and accumulation.
  * Replaces `launch_dense` (kernels.py:193-200; kernel kernels.py:67-98).

@@ -17,7 +17,7 @@ import torch
 
 BLOCK = 64
 MAX_KEY_BLOCKS = 8192
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -42,6 +42,7 @@ _SIGNATURES = {
                            _p, _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
                        _dbl, _p, _p, _p], ctypes.c_int),
+    "sol_plan_protection": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
 }
 
 
@@ -231,6 +232,25 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
         dbg.update(pooled)
         return out, counts, dbg
     return out, counts
+
+
+def plan_protection(rows, keys, key_lengths, local_tokens, ranges):
+    """Packed-block protection of indexed windows on the GPU (``sol_plan_protection``).
+
+    ``rows`` ``[W, nq]`` / ``keys`` ``[W, nk]`` int64, ``key_lengths`` int32
+    ``[W]`` or None, all validated and on one GPU; ``ranges``: sequence of
+    ``(a, b)``.  Returns bool ``[W, NQB, NKB]``.
+    """
+    lib = library()
+    dev = rows.device
+    w, nq = rows.shape
+    nk = keys.shape[1]
+    out = torch.empty((w, -(-nq // BLOCK), -(-nk // BLOCK)), device=dev, dtype=torch.uint8)
+    rng = torch.tensor(list(ranges), dtype=torch.int64).reshape(-1, 2).to(dev) if ranges else None
+    _check(lib.sol_plan_protection(_ptr(rows.contiguous()), _ptr(keys.contiguous()), _ptr(key_lengths),
+                                   w, nq, nk, int(local_tokens), _ptr(rng),
+                                   0 if rng is None else rng.shape[0], _ptr(out), _stream(dev)))
+    return out.view(torch.bool)
 
 
 def launch_dense(q, k, v, scale):

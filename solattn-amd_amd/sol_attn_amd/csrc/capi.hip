@@ -158,6 +158,33 @@ int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* que
   return hip_status(sol::launch_pairing(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
+int sol_plan_protection(const int64_t* rows, const int64_t* keys, const int32_t* key_lengths,
+                        int64_t windows, int64_t query_rows, int64_t key_count,
+                        int64_t local_tokens, const int64_t* ranges, int64_t nranges,
+                        uint8_t* protected_blocks, void* stream) {
+  if (windows <= 0 || query_rows <= 0 || key_count <= 0 || local_tokens < 0 || nranges < 0 ||
+      nranges > (int64_t(1) << 20) || query_rows >= (int64_t(1) << 40) || key_count >= (int64_t(1) << 40))
+    return fail(SOL_ERR_INVALID, "sol_plan_protection: invalid shape or range count");
+  if (!rows || !keys || !protected_blocks || (nranges > 0 && !ranges))
+    return fail(SOL_ERR_INVALID, "sol_plan_protection: rows, keys, ranges and protected_blocks are required");
+  sol::PlanParams p;
+  p.rows = rows;
+  p.keys = keys;
+  p.key_lengths = key_lengths;
+  p.ranges = ranges;
+  p.out = protected_blocks;
+  p.W = windows;
+  p.nq = query_rows;
+  p.nk = key_count;
+  p.NQB = cdiv(query_rows, SOL_BLOCK);
+  p.NKB = cdiv(key_count, SOL_BLOCK);
+  p.local = local_tokens;
+  p.nranges = int(nranges);
+  if (p.W * p.NQB * p.NKB >= (int64_t(1) << 38))  // grid of < 2^30 workgroups
+    return fail(SOL_ERR_INVALID, "sol_plan_protection: plan too large");
+  return hip_status(sol::launch_plan_protection(p, static_cast<hipStream_t>(stream)));
+}
+
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,

@@ -62,9 +62,21 @@ struct AttnParams {
   int kv_sink_blocks, q_sink_blocks;
 };
 
+// Indexed-window protection (plan.hip).
+struct PlanParams {
+  const int64_t* rows;         // [W, nq] sorted original query rows
+  const int64_t* keys;         // [W, nk] sorted original key indices
+  const int32_t* key_lengths;  // [W] keys per window (clamped to nk), or null: nk
+  const int64_t* ranges;       // [nranges, 2] protected ranges [a, b)
+  uint8_t* out;                // [W, NQB, NKB]
+  int64_t W, nq, nk, NQB, NKB, local;
+  int nranges;
+};
+
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream);
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_dense(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream);
+hipError_t launch_plan_protection(const PlanParams& p, hipStream_t stream);
 
 }  // namespace sol

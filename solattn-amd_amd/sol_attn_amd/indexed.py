@@ -43,10 +43,11 @@ def _touches(keys, lo, hi_inclusive, lengths):
     return inside & (val <= hi_inclusive[..., None])
 
 
-def _index_matrix(name, x, sequence_length):
-    if (x.device.type != "cpu" or x.dtype != torch.int64 or x.ndim != 2
+def _index_matrix(name, x, sequence_length, device=torch.device("cpu")):
+    if (x.device != device or x.dtype != torch.int64 or x.ndim != 2
             or any(n == 0 for n in x.shape)):
-        raise ValueError(f"{name} must be a nonempty CPU int64 matrix")
+        where = "CPU" if device.type == "cpu" else f"{device} (the rows' device)"
+        raise ValueError(f"{name} must be a nonempty {where} int64 matrix")
     if bool((x < 0).any() or (x >= sequence_length).any()):
         raise ValueError(f"{name} index outside sequence")
     if bool((x[:, 1:] <= x[:, :-1]).any()):
@@ -80,25 +81,33 @@ class IndexedPlan:
         nonzero lengths (ragged windows, run in one call): the plan then pads
         ``keys`` to the longest window with each window's last key and records
         ``key_lengths``; padded entries are never read.
+
+        With ``rows`` and ``keys`` on the CPU (the reference's contract) the
+        protection is computed on the CPU.  With both on one AMD GPU the plan
+        is built there: the same checks run on the device, the protection
+        comes from the ``sol_plan_protection`` kernel, and the plan is
+        returned on that device (no transfer needed).
         """
         _nonnegative_integer("local_tokens", local_tokens)
         _nonnegative_integer("sequence_length", sequence_length)
         if sequence_length == 0:
             raise ValueError("sequence_length must be positive")
         ragged = isinstance(keys, (list, tuple))
-        _index_matrix("rows", rows, sequence_length)
+        dev = rows.device if isinstance(rows, torch.Tensor) and rows.device.type == "cuda" \
+            else torch.device("cpu")
+        _index_matrix("rows", rows, sequence_length, dev)
         if ragged:
             if len(keys) != rows.shape[0]:
                 raise ValueError("rows and keys must have the same batch size")
             for x in keys:
                 if not isinstance(x, torch.Tensor) or x.ndim != 1:
-                    raise ValueError("ragged keys must be 1-D int64 CPU vectors")
-                _index_matrix("keys", x[None], sequence_length)
+                    raise ValueError("ragged keys must be 1-D int64 vectors on the rows' device")
+                _index_matrix("keys", x[None], sequence_length, dev)
             lengths = torch.tensor([x.numel() for x in keys], dtype=torch.int64)
             nk = int(lengths.max())
             padded = torch.stack([torch.cat((x, x[-1:].expand(nk - x.numel()))) for x in keys])
         else:
-            _index_matrix("keys", keys, sequence_length)
+            _index_matrix("keys", keys, sequence_length, dev)
             if rows.shape[0] != keys.shape[0]:
                 raise ValueError("rows and keys must have the same batch size")
             padded = keys
@@ -110,6 +119,12 @@ class IndexedPlan:
                 raise ValueError("Invalid protected key range")
         rows = rows.clone().contiguous()
         keys = padded.clone().contiguous()
+        if dev.type == "cuda":
+            from ._native import plan_protection
+            key_lengths = lengths.to(torch.int32).to(dev) if ragged else None
+            with torch.cuda.device(dev):
+                protection = plan_protection(rows, keys, key_lengths, local_tokens, ranges)
+            return cls(rows, keys, protection, sequence_length, key_lengths)
         w, nq = rows.shape
         nqb = (nq + BLOCK - 1) // BLOCK
         first = rows[:, ::BLOCK]                                        # [W, NQB]

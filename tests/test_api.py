@@ -127,7 +127,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == 3
+    assert native.sol_abi_version() == 4
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -164,6 +164,14 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     rc = native.sol_pool_kv(fake, strides, fake, strides, None, None, 1, 317, 2, 64, None, None,
                             None, None, None, None)
     assert rc == -1 and b"nothing to write" in native.sol_last_error()
+    rc = native.sol_plan_protection(fake, fake, None, 2, 0, 300, 64, None, 0, fake, None)
+    assert rc == -1 and b"invalid shape" in native.sol_last_error()
+    rc = native.sol_plan_protection(fake, fake, None, 2, 100, 300, -1, None, 0, fake, None)
+    assert rc == -1 and b"invalid shape" in native.sol_last_error()
+    rc = native.sol_plan_protection(fake, fake, None, 2, 100, 300, 64, None, 1, fake, None)
+    assert rc == -1 and b"required" in native.sol_last_error()
+    rc = native.sol_plan_protection(fake, None, None, 2, 100, 300, 64, None, 0, fake, None)
+    assert rc == -1 and b"required" in native.sol_last_error()
 
 
 def test_ragged_plan_matches_oracle_per_window():
