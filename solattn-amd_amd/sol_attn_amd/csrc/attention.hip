@@ -3,8 +3,9 @@
 // Replaces the reference's `_threshold` (src/sol_attn_amd/kernels.py:52-64),
 // `_sol` (kernels.py:101-182) and `_dense` (kernels.py:67-98).
 //
-// SOL workgroup = G adjacent 64-query blocks of one (batch, head), two waves
-// per query block.  Wave w owns query block w >> 1 and its queries
+// SOL workgroup = G 64-query blocks of one (batch, head), paired at the
+// stride the pairing pass chose (adjacent blocks without one), two waves per
+// query block.  Wave w owns query block w >> 1 and its queries
 // 32*(w&1) .. +31, over all 64 keys of every tile, with its own FP32
 // online-softmax state.
 //   1. Q tiles -> LDS -> register fragments (MFMA B operand of S^T = K Q^T)
@@ -95,12 +96,6 @@ __device__ __forceinline__ float pair_sum(float x) {
   const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
 }
-
-// Per-element weight on exp2(s c - m): 1 for exact tokens, the block's valid
-// length for centroids.
-struct UnitWeight {
-  __device__ __forceinline__ float operator()(int, int) const { return 1.f; }
-};
 
 __device__ __forceinline__ bf16x8 pack8(const f32x16& s, int base) {
   u32x4 pb;
