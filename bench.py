@@ -241,6 +241,28 @@ def cpu_baseline(q, k, v, cfg, scale, sample, gpu_out, gpu_sel):
     return t_full, t_sample, threads, parity
 
 
+def threshold_experiment(q, k, v, kw, diag_out, diag_density):
+    """The full-covariance threshold (the reference roadmap's experiment) against
+    the default diagonal estimator, each measured against the BF16 dense
+    control (every key exact): latency, density and output error."""
+    from sol_attn_amd import dense_attention, sol_attention
+    with torch.no_grad():
+        control = dense_attention(q, k, v).float()
+        full_out, full_stats = sol_attention(q, k, v, return_stats=True,
+                                             threshold_estimator="full_covariance", **kw)
+        diag_ms = event_ms(lambda: sol_attention(q, k, v, **kw), 3)
+        full_ms = event_ms(lambda: sol_attention(q, k, v, threshold_estimator="full_covariance", **kw), 3)
+
+        def err(x):
+            delta = x.float() - control
+            return {"rel_l2_vs_dense": (delta.norm() / control.norm()).item(),
+                    "max_abs_vs_dense": delta.abs().max().item()}
+
+        return {"control": "in-house dense BF16 attention (every key exact)",
+                "diagonal_covariance": {"ms": diag_ms, "density": diag_density, **err(diag_out)},
+                "full_covariance": {"ms": full_ms, "density": full_stats.density(), **err(full_out)}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,6 +275,8 @@ def main():
     ap.add_argument("--dense-reps", type=int, default=2)
     ap.add_argument("--no-windows", action="store_true",
                     help="skip the indexed frame-window measurement on the same field")
+    ap.add_argument("--no-threshold-experiment", action="store_true",
+                    help="skip the full- vs diagonal-covariance threshold comparison")
     ap.add_argument("--copy-gib", type=float, default=0.0,
                     help="also run a device copy of this many GiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -345,6 +369,8 @@ def main():
         "pool_roofline": {"bound": "hbm", "achieved": pool_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                           "frac": pool_gbs / PEAK_HBM_GBS, "bytes_per_launch": pool_bytes},
     }
+    if not args.no_threshold_experiment:
+        result["threshold_experiment"] = threshold_experiment(q, k, v, kw, out, density)
     if "frames" in cfg and not args.no_windows:
         result["indexed_windows"] = bench_windows(q, k, v, cfg, max(3, args.steps // 2), not args.no_cpu)
     if not args.no_cpu:

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 4
+#define SOL_ABI_VERSION 5
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
 
@@ -105,11 +105,28 @@ int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* que
                      int64_t batch, int64_t query_tokens, int64_t heads, int64_t head_dim,
                      void* workspace, int32_t* strides, void* stream);
 
+/* Workspace bytes of sol_key_covariance (0: unsupported shape). */
+int64_t sol_key_covariance_workspace_size(int64_t batch, int64_t heads, int64_t head_dim);
+
+/* Full population covariance of the BF16 key centroids per (batch entry,
+ * head): cov = mean_j Kc_j Kc_j^T - mu mu^T, fp32 [batch, heads, head_dim,
+ * head_dim], from the centroid tiles and key_mean of sol_pool_kv (moments
+ * on); key_lengths as in sol_pool_kv.  For the full-covariance threshold
+ * experiment of the reference's roadmap (ROADMAP.md:14-16), which the
+ * reference does not implement; its diagonal is the `_moments` variance
+ * (kernels.py:30-49) before clamping. */
+int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t* key_lengths,
+                       int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
+                       void* workspace, float* key_cov, void* stream);
+
 /* Fused routing + attention over the pooled keys of sol_pool_kv.
  * Replaces the `_threshold` and `_sol` launches of `launch_sol`
  * (kernels.py:203-225; kernels kernels.py:52-64 and 101-182).
  * beta: finite, -INFINITY (every block exact) or +INFINITY (protected blocks
- * only); key_mean/key_var are read only for finite beta.  local_blocks < 0
+ * only); key_mean/key_var are read only for finite beta.  key_cov: NULL (the
+ * reference's diagonal estimator, sqrt(sum Qc^2 var)) or fp32 [batch, heads,
+ * head_dim, head_dim] from sol_key_covariance (the full-covariance threshold
+ * experiment, sqrt(max(Qc^T cov Qc, 0))).  local_blocks < 0
  * disables the local band (indexed windows).  Sink token counts round
  * outward to whole blocks.  protection: NULL or uint8 [batch, NQB, NKB].
  * pair_strides: NULL (adjacent query blocks share a workgroup) or int32
@@ -127,7 +144,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,
                       const void* tiles, const void* ctiles,
-                      const float* key_mean, const float* key_var,
+                      const float* key_mean, const float* key_var, const float* key_cov,
                       const uint8_t* protection, const int32_t* pair_strides,
                       double scale, double beta, int64_t local_blocks,
                       int64_t kv_sink_tokens, int64_t query_sink_tokens,

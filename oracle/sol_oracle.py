@@ -22,7 +22,11 @@ torch ``mean`` (bit-exact) and NumPy ``var``; ``cutoffs``/``route``/``sol_oracle
 vs golden vectors written from the reference oracle, the dense limit (FP32
 SDPA), the prefix-protection known answer ``[5, 2, 3, 3]`` and a float64
 brute force of the virtual-token definition; ``plan_protection`` vs the
-reference's known answers and golden vectors.  No function is parity unpinned.
+reference's known answers and golden vectors; ``key_covariance`` /
+``cutoffs_full`` (the full-covariance threshold experiment of the reference's
+roadmap, which the reference does not implement) vs the identity
+``Qc^T cov Qc = mean_j (Qc . Kc_j)^2 - (Qc . mu)^2``, the diagonal estimator
+when only one feature varies, and beta = 0.  No function is parity unpinned.
 """
 
 from __future__ import annotations
@@ -159,6 +163,40 @@ def cutoffs(qm: np.ndarray, mean: np.ndarray, var: np.ndarray, beta: float,
     return c.astype(np.float32)
 
 
+def key_covariance(kc: np.ndarray) -> np.ndarray:
+    """Full population covariance of pooled keys over the block axis.
+
+    Roadmap item 4 of the reference (``ROADMAP.md:14-16``, "full covariance
+    thresholds"); the reference implements only the diagonal.  The same
+    estimator as ``key_moments`` without discarding the off-diagonal terms:
+    ``cov = mean_j Kc_j Kc_j^T - mu mu^T``, unweighted by ragged length,
+    evaluated in float64.  ``kc``: ``[B, NKB, H, D]`` -> ``[B, H, D, D]``.
+    """
+    kc = np.asarray(kc, dtype=np.float64)
+    n = kc.shape[1]
+    mu = kc.mean(1)                                             # [B, H, D]
+    second = np.einsum("bjhd,bjhe->bhde", kc, kc) / n
+    return (second - mu[..., :, None] * mu[..., None, :]).astype(np.float32)
+
+
+def cutoffs_full(qm: np.ndarray, mean: np.ndarray, cov: np.ndarray, beta: float,
+                 scale: float) -> np.ndarray:
+    """Eq. 15 cutoff with the full covariance, natural-log units:
+    ``scale * (Qc . mu + beta * sqrt(max(Qc^T cov Qc, 0)))`` (float64
+    quadratic form; the clamp absorbs rounding below zero).
+    ``qm``: ``[B, NQB, H, D]``; ``mean``: ``[B, H, D]``; ``cov``: ``[B, H, D, D]``.
+    """
+    q64 = np.asarray(qm, dtype=np.float64)
+    mu = (q64 * np.asarray(mean, dtype=np.float64)[:, None]).sum(-1)
+    quad = np.einsum("bqhd,bhde,bqhe->bqh", q64, np.asarray(cov, dtype=np.float64), q64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        c = (mu + beta * np.sqrt(np.maximum(quad, 0.0))) * scale
+    return c.astype(np.float32)
+
+
+THRESHOLD_ESTIMATORS = ("diagonal_covariance", "full_covariance")
+
+
 # ----------------------------------------------------------------------------
 # Routing
 # ----------------------------------------------------------------------------
@@ -253,7 +291,8 @@ def _attend(qrows, k, v, kc, vc, sel_rows, lengths, scale, dtype):
 def sol_oracle(q, k, v, *, beta: float = 1.0, scale: Optional[float] = None,
                local_blocks: int = 1, kv_sink_tokens: int = 0, query_sink_tokens: int = 0,
                protected_blocks=None, query_blocks: Optional[Iterable[int]] = None,
-               selected: Optional[np.ndarray] = None, dtype=np.float32):
+               selected: Optional[np.ndarray] = None, dtype=np.float32,
+               threshold_estimator: str = "diagonal_covariance"):
     """FP32 SOL oracle, ``reference.py:18-66`` restated.
 
     ``q``: ``[B, Tq, H, D]``; ``k``/``v``: ``[B, Tk, H, D]``; BF16 values held
@@ -264,6 +303,8 @@ def sol_oracle(q, k, v, *, beta: float = 1.0, scale: Optional[float] = None,
     forces the routing (``[B, NQB, H, NKB]``) so outputs can be compared
     under identical routing.  ``dtype=np.float64`` evaluates the same
     definition in double precision (brute-force check).
+    ``threshold_estimator="full_covariance"`` replaces the diagonal variance
+    of the cutoff with the full key covariance (``cutoffs_full``).
 
     Returns ``out`` (float32, NaN outside ``query_blocks``), ``counts``
     (int32 ``[B, NQB, H]``, -1 outside ``query_blocks``) and an ``info`` dict
@@ -278,7 +319,14 @@ def sol_oracle(q, k, v, *, beta: float = 1.0, scale: Optional[float] = None,
     kc = block_means(k, round_bf16=True)
     vc = block_means(v, round_bf16=True)
     mean, var = key_moments(kc)
-    cut = cutoffs(qm, mean, var, beta, scale)
+    if threshold_estimator not in THRESHOLD_ESTIMATORS:
+        raise ValueError(f"threshold_estimator must be one of {THRESHOLD_ESTIMATORS}")
+    cov = None
+    if threshold_estimator == "full_covariance":
+        cov = key_covariance(kc)
+        cut = cutoffs_full(qm, mean, cov, beta, scale)
+    else:
+        cut = cutoffs(qm, mean, var, beta, scale)
     nqb, nkb = qm.shape[1], kc.shape[1]
     prot = None if protected_blocks is None else _as_bool(protected_blocks)
     sel, proxy = route(q, kc, cut, beta=beta, scale=scale, local_blocks=local_blocks,
@@ -301,7 +349,7 @@ def sol_oracle(q, k, v, *, beta: float = 1.0, scale: Optional[float] = None,
                 out[bi, rows, hi] = res.astype(np.float32)
                 for qb in chunk:
                     counts[bi, qb, hi] = int(sel[bi, qb, hi].sum())
-    info = dict(selected=sel, proxy=proxy, cutoff=cut, kc=kc, vc=vc, qm=qm, mean=mean, var=var)
+    info = dict(selected=sel, proxy=proxy, cutoff=cut, kc=kc, vc=vc, qm=qm, mean=mean, var=var, cov=cov)
     return out, counts, info
 
 

@@ -17,7 +17,7 @@ import torch
 
 BLOCK = 64
 MAX_KEY_BLOCKS = 8192
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -37,12 +37,14 @@ _SIGNATURES = {
     "sol_pair_workspace_size": ([_i64, _i64, _i64, _i64], ctypes.c_int64),
     "sol_pair_strides": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _p, _i64, _i64,
-                           _p, _p, _p, _p, _p, _p,
+                           _p, _p, _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
                            _p, _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
                        _dbl, _p, _p, _p], ctypes.c_int),
     "sol_plan_protection": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
+    "sol_key_covariance_workspace_size": ([_i64, _i64, _i64], ctypes.c_int64),
+    "sol_key_covariance": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
 }
 
 
@@ -133,6 +135,25 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None):
             "key_blocks": nkb, "key_lengths": key_lengths}
 
 
+def key_covariance(pooled):
+    """Adds ``pooled["cov"]``: the full covariance of the key centroids, fp32
+    ``[B, H, D, D]`` (``sol_key_covariance``), for the full-covariance
+    threshold.  ``pooled`` must come from :func:`pool_kv` with moments."""
+    if pooled["mean"] is None:
+        raise ValueError("the full-covariance threshold needs the key moments (finite beta)")
+    lib = library()
+    ctiles = pooled["ctiles"]
+    b, h, _, _, e = ctiles.shape
+    d = e // BLOCK
+    dev = ctiles.device
+    work = torch.empty(lib.sol_key_covariance_workspace_size(b, h, d) // 4, device=dev, dtype=torch.float32)
+    cov = torch.empty((b, h, d, d), device=dev, dtype=torch.float32)
+    _check(lib.sol_key_covariance(_ptr(ctiles), _ptr(pooled["mean"]), _ptr(pooled.get("key_lengths")),
+                                  b, pooled["key_tokens"], h, d, _ptr(work), _ptr(cov), _stream(dev)))
+    pooled["cov"] = cov
+    return pooled
+
+
 # Pair query blocks by the stride sol_pair_strides picks (False: adjacent
 # blocks share a workgroup).  Results are identical either way.
 PAIRING = True
@@ -205,7 +226,7 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     _check(lib.sol_attention_fwd(
         _ptr(q), _strides(q, indexed), _ptr(rows), b, nq, nk, _ptr(pooled.get("key_lengths")), h, d,
         _ptr(pooled["tiles"]), _ptr(pooled["ctiles"]),
-        _ptr(pooled["mean"]), _ptr(pooled["var"]),
+        _ptr(pooled["mean"]), _ptr(pooled["var"]), _ptr(pooled.get("cov")),
         _ptr(prot), _ptr(strides), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
         _ptr(out), _ptr(rows if scatter else None), _ptr(counts),
         _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
@@ -216,16 +237,21 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
 
 
 def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=None,
-               rows=None, keys=None, debug=False, key_lengths=None, out=None):
+               rows=None, keys=None, debug=False, key_lengths=None, out=None,
+               threshold_estimator="diagonal_covariance"):
     """All-in SOL attention (``kernels.py:203-225``): pooling, moments, routing, attention.
 
     ``rows``/``keys`` (indexed windows) gather Q and K/V token rows inside the
     kernels instead of materialising copies; ``key_lengths`` makes the windows'
     key counts ragged and ``out`` scatters the result rows (see :func:`attend`).
+    ``threshold_estimator="full_covariance"`` builds the cutoff from the full
+    key covariance (:func:`key_covariance`) instead of its diagonal.
     Returns ``(out, counts)`` and, with ``debug=True``, a dict of routing
     diagnostics as a third element.
     """
     pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths)
+    if threshold_estimator == "full_covariance" and not math.isinf(beta):
+        key_covariance(pooled)
     out, counts, dbg = attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection, rows,
                               debug, out)
     if debug:

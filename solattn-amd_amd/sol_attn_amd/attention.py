@@ -72,8 +72,18 @@ def dense_attention(q, k, v, *, scale=None):
         return launch_dense(q, k, v, scale)
 
 
+THRESHOLD_ESTIMATORS = ("diagonal_covariance", "full_covariance")
+
+
+def _threshold_estimator(name):
+    if name not in THRESHOLD_ESTIMATORS:
+        raise ValueError("threshold_estimator must be 'diagonal_covariance' or 'full_covariance'")
+    return name
+
+
 def sol_attention(q, k, v, *, beta=1.0, scale=None, local_blocks=1,
-                  kv_sink_tokens=0, query_sink_tokens=0, return_stats=False):
+                  kv_sink_tokens=0, query_sink_tokens=0, return_stats=False,
+                  threshold_estimator="diagonal_covariance"):
     """SOL-style noncausal attention (``attention.py:58-85``).
 
     Physical blocks hold 64 tokens.  Selected blocks use BF16 QK/PV with FP32
@@ -82,11 +92,18 @@ def sol_attention(q, k, v, *, beta=1.0, scale=None, local_blocks=1,
     diagonal-covariance estimator (paper Eq. 15).  Prefix protection rounds
     outward to whole blocks.  beta=-inf forces every block exact; beta=+inf
     leaves only protected blocks exact.
+
+    ``threshold_estimator="full_covariance"`` (not in the reference: the
+    full-covariance threshold experiment of its roadmap) replaces
+    ``sqrt(sum Qc^2 var)`` with ``sqrt(max(Qc^T cov Qc, 0))`` over the full
+    covariance of the key centroids; the default keeps the reference's
+    diagonal estimator.
     """
     scale = _validate(q, k, v, scale)
     beta = float(beta)
     if math.isnan(beta):
         raise ValueError("beta must not be NaN")
+    _threshold_estimator(threshold_estimator)
     for name, value in (("local_blocks", local_blocks),
                         ("kv_sink_tokens", kv_sink_tokens),
                         ("query_sink_tokens", query_sink_tokens)):
@@ -96,7 +113,8 @@ def sol_attention(q, k, v, *, beta=1.0, scale=None, local_blocks=1,
     from ._native import launch_sol
     with torch.no_grad(), torch.cuda.device(q.device):
         out, counts = launch_sol(q, k, v, scale, beta, local_blocks,
-                                 kv_sink_tokens, query_sink_tokens, return_stats)
+                                 kv_sink_tokens, query_sink_tokens, return_stats,
+                                 threshold_estimator=threshold_estimator)
     if return_stats:
         return out, SolStats(counts, (k.shape[1] + 63) // 64)
     return out

@@ -738,7 +738,15 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
     if (lt < D) {
       const float qm = s_qm[qg][lt];
       a = qm * p.mean[head * D + lt];
-      g = qm * qm * p.var[head * D + lt];
+      if (p.cov) {
+        // Full covariance: this feature's term of Qc^T cov Qc.
+        const float* row = p.cov + (head * D + lt) * D;
+        float sq = 0.f;
+        for (int e = 0; e < D; ++e) sq = fmaf(row[e], s_qm[qg][e], sq);
+        g = qm * sq;
+      } else {
+        g = qm * qm * p.var[head * D + lt];
+      }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -750,7 +758,10 @@ __global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p)
       s_red[qg][2 + qh] = g;
     }
     __syncthreads();
-    if (tid < G) s_cut[tid] = (s_red[tid][0] + s_red[tid][1]) + p.beta * sqrtf(s_red[tid][2] + s_red[tid][3]);
+    if (tid < G) {
+      const float quad = s_red[tid][2] + s_red[tid][3];  // the full quadratic form may round below 0
+      s_cut[tid] = (s_red[tid][0] + s_red[tid][1]) + p.beta * sqrtf(p.cov ? fmaxf(quad, 0.f) : quad);
+    }
   }
   __syncthreads();  // cutoffs published; Q staging is dead and the ring is free
   const int64_t dbg_row = ((int64_t(b) * p.NQB + qb) * p.H + h) * p.NKB;

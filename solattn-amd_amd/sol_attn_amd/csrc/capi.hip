@@ -185,11 +185,39 @@ int sol_plan_protection(const int64_t* rows, const int64_t* keys, const int32_t*
   return hip_status(sol::launch_plan_protection(p, static_cast<hipStream_t>(stream)));
 }
 
+int64_t sol_key_covariance_workspace_size(int64_t batch, int64_t heads, int64_t head_dim) {
+  if (!shape_ok(batch, 1, heads, head_dim)) return 0;
+  return batch * heads * sol::kCovSplit * head_dim * head_dim * 4;
+}
+
+int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t* key_lengths,
+                       int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
+                       void* workspace, float* key_cov, void* stream) {
+  if (!shape_ok(batch, key_tokens, heads, head_dim))
+    return fail(SOL_ERR_INVALID, "sol_key_covariance: invalid shape");
+  if (!ctiles || !aligned16(ctiles) || !key_mean || !workspace || !key_cov)
+    return fail(SOL_ERR_INVALID, "sol_key_covariance: ctiles (16-byte aligned), key_mean, workspace and key_cov are required");
+  const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
+  if (nkb > SOL_MAX_KEY_BLOCKS)
+    return fail(SOL_ERR_UNSUPPORTED, "sol_key_covariance: key_tokens exceeds 64 * SOL_MAX_KEY_BLOCKS");
+  sol::CovParams p;
+  p.ctiles = static_cast<const uint16_t*>(ctiles);
+  p.mean = key_mean;
+  p.klen = key_lengths;
+  p.partial = static_cast<float*>(workspace);
+  p.cov = key_cov;
+  p.B = int(batch);
+  p.H = int(heads);
+  p.Tk = int(key_tokens);
+  p.NCT = int(cdiv(nkb, SOL_BLOCK));
+  return hip_status(sol::launch_covariance(p, int(head_dim), static_cast<hipStream_t>(stream)));
+}
+
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,
                       const void* tiles, const void* ctiles, const float* key_mean,
-                      const float* key_var, const uint8_t* protection,
+                      const float* key_var, const float* key_cov, const uint8_t* protection,
                       const int32_t* pair_strides, double scale, double beta,
                       int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
@@ -226,6 +254,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   p.ctiles = static_cast<const uint16_t*>(ctiles);
   p.mean = key_mean;
   p.var = key_var;
+  p.cov = force == 0 ? key_cov : nullptr;
   p.protection = protection;
   p.out = static_cast<uint16_t*>(out);
   p.counts = counts;

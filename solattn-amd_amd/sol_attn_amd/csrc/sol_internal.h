@@ -28,6 +28,19 @@ struct PoolParams {
                                  // (NKB, NCT: for Tk; ragged entries use a prefix)
 };
 
+// Full key covariance (covariance.hip): the full-covariance threshold
+// experiment.  Partial sums over kCovSplit centroid ranges per (entry, head).
+constexpr int kCovSplit = 16;
+
+struct CovParams {
+  const uint16_t* ctiles;  // [B, H, NCT, 2, 64 * D] centroid tiles (K halves read)
+  const float* mean;       // [B, H, D] key centroid means
+  const int32_t* klen;     // [B] key tokens per entry, or null: all Tk
+  float* partial;          // [B, H, kCovSplit, D, D] workspace
+  float* cov;              // [B, H, D, D]
+  int B, H, Tk, NCT;
+};
+
 // Query-block pairing (pairing.hip).
 constexpr int kMaxLag = 256;           // strides considered: 1 .. kMaxLag
 constexpr int kMaxPairBlocks = 8192;   // query blocks per (entry, head) the lag kernel holds in LDS
@@ -49,6 +62,7 @@ struct AttnParams {
   const uint16_t* ctiles;      // [B, H, NCT, 2, 64 * D] centroid tiles
   const float* mean;           // [B, H, D]
   const float* var;            // [B, H, D]
+  const float* cov;            // [B, H, D, D] full key covariance, or null: diagonal (var)
   const uint8_t* protection;   // [B, NQB, NKB] or null
   uint16_t* out;               // [B, Tq, H, D], or [N, H, D] rows out_index
   int32_t* counts;             // [B, NQB, H] or null
@@ -78,5 +92,6 @@ hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_dense(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream);
 hipError_t launch_plan_protection(const PlanParams& p, hipStream_t stream);
+hipError_t launch_covariance(const CovParams& p, int D, hipStream_t stream);
 
 }  // namespace sol

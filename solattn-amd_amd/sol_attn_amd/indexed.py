@@ -18,7 +18,7 @@ import math
 
 import torch
 
-from .attention import SolStats, _validate, _nonnegative_integer
+from .attention import SolStats, _validate, _nonnegative_integer, _threshold_estimator
 
 BLOCK = 64
 
@@ -143,7 +143,8 @@ class IndexedPlan:
                            None if self.key_lengths is None else self.key_lengths.to(device))
 
 
-def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=False, out=None):
+def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=False, out=None,
+                          threshold_estimator="diagonal_covariance"):
     """BF16 NHD inputs -> ``[windows, query_rows, heads, D]`` (``indexed.py:69-104``).
 
     Window ``w`` attends its query rows ``plan.rows[w]`` to its keys
@@ -157,6 +158,8 @@ def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=F
     step of a window adapter fused into the kernel's store -- and ``out`` is
     returned; other rows of ``out`` are left as they were.  Rows shared by
     two windows of one plan would race, so a plan's rows must be distinct.
+
+    ``threshold_estimator``: as in :func:`sol_attention`.
     """
     if any(t.ndim != 3 for t in (q, k, v)) or q.shape != k.shape or k.shape != v.shape:
         raise ValueError("Indexed Q/K/V must have matching NHD shapes")
@@ -185,11 +188,13 @@ def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=F
     beta = float(beta)
     if math.isnan(beta):
         raise ValueError("beta must not be NaN")
+    _threshold_estimator(threshold_estimator)
     from ._native import launch_sol
     with torch.no_grad(), torch.cuda.device(q.device):
         result, counts = launch_sol(q, k, v, scale, beta, -1, 0, 0, return_stats,
                                     plan.protected_blocks, rows=plan.rows, keys=plan.keys,
-                                    key_lengths=lengths, out=out)
+                                    key_lengths=lengths, out=out,
+                                    threshold_estimator=threshold_estimator)
     if return_stats:
         key_blocks = ((plan.keys.shape[1] + 63) // 64 if lengths is None
                       else (lengths.to(torch.int64) + 63) // 64)

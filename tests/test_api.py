@@ -127,7 +127,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == 4
+    assert native.sol_abi_version() == 5
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -150,7 +150,7 @@ def test_c_abi_rejects_bad_arguments_without_launching():
                               float("nan"), fake, fake, None)
     assert rc == -1 and b"scale" in native.sol_last_error()
     rc = native.sol_attention_fwd(fake, strides, None, 1, 193, 317, None, 2, 64, fake, fake,
-                                  None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None,
+                                  None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None,
                                   None, None, None, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
     rc = native.sol_pair_strides(fake, strides, None, 1, 192, 2, 64, fake, fake, None)
@@ -164,6 +164,12 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     rc = native.sol_pool_kv(fake, strides, fake, strides, None, None, 1, 317, 2, 64, None, None,
                             None, None, None, None)
     assert rc == -1 and b"nothing to write" in native.sol_last_error()
+    assert native.sol_key_covariance_workspace_size(2, 3, 64) == 2 * 3 * 16 * 64 * 64 * 4
+    assert native.sol_key_covariance_workspace_size(2, 3, 96) == 0
+    rc = native.sol_key_covariance(fake, fake, None, 1, 317, 2, 96, fake, fake, None)
+    assert rc == -1 and b"invalid shape" in native.sol_last_error()
+    rc = native.sol_key_covariance(fake, None, None, 1, 317, 2, 64, fake, fake, None)
+    assert rc == -1 and b"required" in native.sol_last_error()
     rc = native.sol_plan_protection(fake, fake, None, 2, 0, 300, 64, None, 0, fake, None)
     assert rc == -1 and b"invalid shape" in native.sol_last_error()
     rc = native.sol_plan_protection(fake, fake, None, 2, 100, 300, -1, None, 0, fake, None)

@@ -109,28 +109,31 @@ def test_pooling_strided_and_indexed_gather():
     np.testing.assert_array_equal(to_np(out["var"]), var)
 
 
-def run_debug(q, k, v, beta, scale=None, local=1, kv_sink=0, q_sink=0):
+def run_debug(q, k, v, beta, scale=None, local=1, kv_sink=0, q_sink=0, estimator="diagonal_covariance"):
     scale = q.shape[-1] ** -0.5 if scale is None else scale
     with torch.no_grad():
         out, counts, dbg = _native.launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, True,
-                                              debug=True)
+                                              debug=True, threshold_estimator=estimator)
     torch.cuda.synchronize()
     return out, counts, dbg
 
 
 def check_routing(q, k, v, beta, scale=None, local=1, kv_sink=0, q_sink=0, query_blocks=None,
-                  max_band_mismatch=None):
+                  max_band_mismatch=None, estimator="diagonal_covariance"):
     """Decisions vs oracle (band), outputs under identical routing, counts.
 
     Returns ``(kernel_out, oracle_out_under_kernel_routing, qrows)``."""
     qn, kn, vn = to_np(q.cpu()), to_np(k.cpu()), to_np(v.cpu())
     d = qn.shape[-1]
     s = d ** -0.5 if scale is None else scale
-    out, counts, dbg = run_debug(q, k, v, beta, s, local, kv_sink, q_sink)
+    out, counts, dbg = run_debug(q, k, v, beta, s, local, kv_sink, q_sink, estimator)
     qm = orc.block_means(qn, False)
     kc = orc.block_means(kn, True)
     mean, var = orc.key_moments(kc)
-    cut = orc.cutoffs(qm, mean, var, beta, s)
+    if estimator == "full_covariance":
+        cut = orc.cutoffs_full(qm, mean, orc.key_covariance(kc), beta, s)
+    else:
+        cut = orc.cutoffs(qm, mean, var, beta, s)
     sel, proxy = orc.route(qn, kc, cut, beta=beta, scale=s, local_blocks=local,
                            kv_sink_tokens=kv_sink, query_sink_tokens=q_sink, query_blocks=query_blocks)
     ksel = to_np(dbg["selected"]).astype(bool)

@@ -241,3 +241,52 @@ def test_forced_routing_reproduces_given_decisions():
     np.testing.assert_array_equal(counts, forced.sum(-1))
     brute = _virtual_token_bruteforce(q, k, v, forced, 64 ** -0.5)
     np.testing.assert_allclose(out, brute, atol=2e-6, rtol=1e-5)
+
+
+# Full-covariance thresholds (roadmap item 4 of the reference; no reference
+# implementation exists, so the estimator is pinned by independent identities).
+
+def _smooth_keys(seed, nkb=37, h=2, d=16):
+    rng = np.random.default_rng(seed)
+    base = rng.standard_normal((1, nkb, h, d))
+    mix = rng.standard_normal((d, d)) * 0.4                 # correlated features
+    return orc.bf16_round((base @ mix + 0.3).astype(np.float32))
+
+
+def test_full_covariance_quadratic_form_identity():
+    kc = _smooth_keys(3)
+    cov = orc.key_covariance(kc)
+    assert cov.shape == (1, 2, 16, 16)
+    np.testing.assert_allclose(cov, np.swapaxes(cov, -1, -2), rtol=0, atol=1e-6)
+    rng = np.random.default_rng(4)
+    qm = rng.standard_normal((1, 5, 2, 16)).astype(np.float32)
+    k64 = kc.astype(np.float64)
+    proj = np.einsum("bqhd,bjhd->bqhj", qm.astype(np.float64), k64)      # Qc . Kc_j
+    mu = proj.mean(-1)
+    quad = (proj ** 2).mean(-1) - mu ** 2                                 # E[(Qc.Kc)^2] - (Qc.mu)^2
+    mean, _ = orc.key_moments(kc)
+    got = orc.cutoffs_full(qm, mean, cov, beta=1.0, scale=1.0) - orc.cutoffs_full(qm, mean, cov, 0.0, 1.0)
+    np.testing.assert_allclose(got, np.sqrt(np.maximum(quad, 0)), rtol=2e-5, atol=1e-5)
+
+
+def test_full_covariance_equals_diagonal_when_one_feature_varies():
+    rng = np.random.default_rng(5)
+    kc = np.tile(rng.standard_normal((1, 1, 2, 16)), (1, 29, 1, 1))
+    kc[..., 3] += rng.standard_normal((1, 29, 2))
+    kc = orc.bf16_round(kc.astype(np.float32))
+    qm = rng.standard_normal((1, 4, 2, 16)).astype(np.float32)
+    mean, var = orc.key_moments(kc)
+    full = orc.cutoffs_full(qm, mean, orc.key_covariance(kc), 1.5, 0.125)
+    diag = orc.cutoffs(qm, mean, var, 1.5, 0.125)
+    np.testing.assert_allclose(full, diag, rtol=1e-5, atol=1e-6)
+
+
+def test_full_covariance_beta_zero_and_oracle_option():
+    rng = np.random.default_rng(6)
+    q, k, v = (orc.bf16_round(rng.standard_normal((1, 200, 2, 64)).astype(np.float32)) for _ in range(3))
+    a, ca, ia = orc.sol_oracle(q, k, v, beta=0.0)
+    b, cb, ib = orc.sol_oracle(q, k, v, beta=0.0, threshold_estimator="full_covariance")
+    np.testing.assert_allclose(ia["cutoff"], ib["cutoff"], rtol=1e-5, atol=1e-6)
+    assert ib["cov"].shape == (1, 2, 64, 64) and ia["cov"] is None
+    with pytest.raises(ValueError):
+        orc.sol_oracle(q, k, v, threshold_estimator="banded")
