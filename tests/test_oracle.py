@@ -290,3 +290,32 @@ def test_full_covariance_beta_zero_and_oracle_option():
     assert ib["cov"].shape == (1, 2, 64, 64) and ia["cov"] is None
     with pytest.raises(ValueError):
         orc.sol_oracle(q, k, v, threshold_estimator="banded")
+
+
+def test_quantised_qk_accuracy_against_bf16_control():
+    """The INT8 / FP8 QK half of the reference roadmap's experiment row, in
+    simulation: attention with Q and K rounded to FP8-e4m3, or to INT8 with one
+    symmetric scale per row, against the same attention on the BF16 inputs
+    (float64 softmax).  FP8 QK lands far outside the parity bar (rel-L2 0.8%);
+    per-row INT8 sits at it."""
+    rng = np.random.default_rng(0)
+    t, d = 1024, 128
+
+    def fp8(x):
+        return torch.from_numpy(x.astype(np.float32)).to(torch.float8_e4m3fn).float().numpy()
+
+    def int8_rows(x):
+        s = np.abs(x).max(1, keepdims=True) / 127.0
+        return np.clip(np.round(x / s), -127, 127) * s
+
+    def attn(q, k, v):
+        s = q.astype(np.float64) @ k.T.astype(np.float64) / math.sqrt(d)
+        p = np.exp(s - s.max(1, keepdims=True))
+        return (p / p.sum(1, keepdims=True)) @ v
+
+    q, k, v = (orc.bf16_round(rng.standard_normal((t, d)).astype(np.float32)) for _ in range(3))
+    ref = attn(q, k, v)
+    err = {name: np.linalg.norm(attn(f(q), f(k), v) - ref) / np.linalg.norm(ref)
+           for name, f in (("fp8", fp8), ("int8", int8_rows))}
+    assert 0.02 < err["fp8"] < 0.06, err
+    assert 0.004 < err["int8"] < 0.012, err
