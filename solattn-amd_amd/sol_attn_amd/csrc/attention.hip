@@ -27,6 +27,8 @@
 // units; empty states use max 0 for the rescale (kernels.py:148-150).
 // The dense control streams every exact tile, 128 queries per workgroup
 // (4 waves x 32 queries, full 64-key tiles per wave).
+#include <cstdlib>
+
 #include "sol_device.h"
 #include "sol_internal.h"
 
@@ -668,8 +670,11 @@ __device__ __forceinline__ int slot_block(int s, int n, int stride) {
 // __launch_bounds__ second argument: minimum waves per SIMD.  Two waves per
 // SIMD leave each wave 256 VGPRs: the exact path keeps the 64-register
 // accumulator, 32 registers of Q fragments and 64 of K or V fragments live.
+// The bound names 256 threads for both workgroup forms, so the one-block form
+// (128 threads) is held to the same budget (with its own 128-thread bound the
+// compiler moves values through AGPRs instead).
 template <int D, int G, int R>
-__global__ __launch_bounds__(128 * G, 2) void sol_attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   using S = Shape<D>;
   using TL = TileLayout<D>;
   constexpr int NT = 128 * G;
@@ -920,24 +925,30 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   store_output<D>(p, b, h, q0 + myq, hh, st);
 }
 
-// Query blocks per workgroup and LDS ring depth of the SOL kernel.
-#ifndef SOL_GROUP
-#define SOL_GROUP 2
-#endif
-#ifndef SOL_RING
-#define SOL_RING 2
-#endif
-constexpr int kSolGroup = SOL_GROUP;
-constexpr int kSolRing = SOL_RING;
+// LDS ring depth of the SOL kernel.
+constexpr int kSolRing = 2;
+// Below this many two-block workgroups the launch leaves CUs idle (256 CUs x
+// 2 workgroups): such launches run one query block per workgroup instead,
+// which doubles the workgroups and has no union to stream.  Both forms give
+// bit-identical results (a wave's tiles, their order and its softmax state
+// do not depend on its partner).  SOL_ATTN_GROUP=1 or 2 in the environment
+// forces one form (for tests and tuning).
+constexpr int64_t kSmallLaunchGroups = 512;
+
+template <int D, int G>
+void launch_sol_group(const AttnParams& p, hipStream_t stream) {
+  const unsigned grid = xcd_grid(p.B * p.H, (p.NQB + G - 1) / G);
+  hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing>), dim3(grid), dim3(128 * G), 0, stream, p);
+}
 
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
-  const unsigned grid = xcd_grid(p.B * p.H, (p.NQB + kSolGroup - 1) / kSolGroup);
-  if (D == 128)
-    hipLaunchKernelGGL((sol_attention_kernel<128, kSolGroup, kSolRing>), dim3(grid),
-                       dim3(128 * kSolGroup), 0, stream, p);
-  else
-    hipLaunchKernelGGL((sol_attention_kernel<64, kSolGroup, kSolRing>), dim3(grid),
-                       dim3(128 * kSolGroup), 0, stream, p);
+  int g = int64_t(p.B) * p.H * ((p.NQB + 1) / 2) < kSmallLaunchGroups ? 1 : 2;
+  if (const char* forced = std::getenv("SOL_ATTN_GROUP")) g = std::atoi(forced) == 1 ? 1 : 2;
+  if (D == 128) {
+    if (g == 1) launch_sol_group<128, 1>(p, stream); else launch_sol_group<128, 2>(p, stream);
+  } else {
+    if (g == 1) launch_sol_group<64, 1>(p, stream); else launch_sol_group<64, 2>(p, stream);
+  }
   return hipGetLastError();
 }
 

@@ -105,3 +105,18 @@ def test_indexed_windows_pair_per_window(monkeypatch):
     ref = sol_attention_indexed(*x, plan, beta=1.0)
     monkeypatch.setattr(_native, "PAIRING", False)
     assert torch.equal(ref, sol_attention_indexed(*x, plan, beta=1.0))
+
+
+@pytest.mark.parametrize("shape", [(1, 4096, 4, 128), (2, 1000, 3, 64), (1, 20000, 2, 128)])
+def test_one_and_two_block_workgroups_are_identical(shape, monkeypatch):
+    """Small launches run one query block per workgroup; both forms must give
+    bit-identical outputs and counts (a wave's tiles and their order do not
+    depend on its partner block)."""
+    b, t, h, d = shape
+    q, k, v = (frames(-(-t // 576), 9, heads=h, d=d, seed=s)[:, :t].repeat(b, 1, 1, 1).cuda() for s in (12, 13, 14))
+    res = {}
+    for g in ("1", "2"):
+        monkeypatch.setenv("SOL_ATTN_GROUP", g)
+        res[g] = sol_attention(q, k, v, beta=1.0, kv_sink_tokens=64, return_stats=True)
+    assert torch.equal(res["1"][0], res["2"][0])
+    assert torch.equal(res["1"][1].exact_blocks, res["2"][1].exact_blocks)
