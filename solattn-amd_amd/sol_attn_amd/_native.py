@@ -2,8 +2,8 @@
 
 Mirrors ``src/sol_attn_amd/kernels.py:185-225``: ``launch_sol`` and
 ``launch_dense`` take validated BF16 tensors, allocate every output and
-workspace with ``torch.empty`` on the input device, and enqueue the HIP
-kernels on the current stream.  There is no CPU path: when the library is not
+workspace with ``torch.empty`` on the input device (the pooled key buffers
+as one workspace), and enqueue the HIP kernels on the current stream.  There is no CPU path: when the library is not
 built this module raises.
 """
 
@@ -79,11 +79,18 @@ def _strides(x, indexed=False):
 
 
 def _ptr(x):
-    return None if x is None else ctypes.c_void_p(x.data_ptr())
+    # ctypes passes a Python int (or None, NULL) for a c_void_p argument.
+    return None if x is None else x.data_ptr()
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def _stream(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The device's current stream as a ``hipStream_t`` value."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def _aligned(x):
@@ -100,13 +107,32 @@ def _tiles(b, h, nkb, d, device):
     return torch.empty((b, h, nkb, 2, BLOCK * d), device=device, dtype=torch.bfloat16)
 
 
-def pool_kv(k, v, key_index=None, moments=True, key_lengths=None):
+_ALIGN = 256  # byte alignment of each buffer carved from a workspace
+
+
+def _carve(sizes):
+    """Byte offsets of consecutive ``_ALIGN``-aligned regions, and their total."""
+    offsets, total = [], 0
+    for n in sizes:
+        offsets.append(total)
+        total += -(-n // _ALIGN) * _ALIGN
+    return offsets, total
+
+
+def _region(ws, offset, dtype, shape):
+    n = math.prod(shape) * torch.empty((), dtype=dtype).element_size()
+    return ws[offset:offset + n].view(dtype).view(shape)
+
+
+def pool_kv(k, v, key_index=None, moments=True, key_lengths=None, stream=None, views=True):
     """Centroid tiles, attention tiles and key moments (one HBM pass over K and V).
 
     ``k``/``v``: ``[B, Tk, H, D]`` BF16 or, with ``key_index`` ``[B, Tk]``,
     NHD ``[N, H, D]``.  ``key_lengths`` (int32 ``[B]`` on the device, ragged
-    windows): entry b uses its first ``key_lengths[b]`` keys.  Returns a dict
-    with ``ctiles`` ``[B, H, NCT, 2, 64 D]`` (block centroids), ``tiles``
+    windows): entry b uses its first ``key_lengths[b]`` keys.  All buffers are
+    carved from one workspace allocation.  Returns a dict with the workspace,
+    the buffers' device addresses (``*_ptr``) and, with ``views``, tensor views
+    ``ctiles`` ``[B, H, NCT, 2, 64 D]`` (block centroids), ``tiles``
     ``[B, H, NKB, 2, 64 D]`` and ``mean``/``var`` ``[B, H, D]`` (None without
     ``moments``); layouts per ``include/sol_attn_amd.h``.
     """
@@ -121,36 +147,48 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None):
     nkb = -(-tk // BLOCK)
     nct = -(-nkb // BLOCK)
     dev = k.device
-    ctiles = _tiles(b, h, nct, d, dev)
-    tiles = _tiles(b, h, nkb, d, dev)
-    mean = var = sums = None
+    if stream is None:
+        stream = _stream(dev)
+    tile = 2 * BLOCK * d * 2  # bytes of one K/V tile pair
+    sizes = [b * h * nct * tile, b * h * nkb * tile]
     if moments:
-        sums = torch.empty((b, h, -(-nkb // 16), 2, d), device=dev, dtype=torch.float32)
-        mean = torch.empty((b, h, d), device=dev, dtype=torch.float32)
-        var = torch.empty_like(mean)
-    _check(lib.sol_pool_kv(_ptr(k), _strides(k, indexed), _ptr(v), _strides(v, indexed),
-                           _ptr(key_index), _ptr(key_lengths), b, tk, h, d, _ptr(ctiles),
-                           _ptr(tiles), _ptr(sums), _ptr(mean), _ptr(var), _stream(dev)))
-    return {"ctiles": ctiles, "tiles": tiles, "mean": mean, "var": var, "key_tokens": tk,
-            "key_blocks": nkb, "key_lengths": key_lengths}
+        sizes += [b * h * -(-nkb // 16) * 2 * d * 4, b * h * d * 4, b * h * d * 4]
+    offsets, total = _carve(sizes)
+    ws = torch.empty(total, device=dev, dtype=torch.uint8)
+    base = ws.data_ptr()
+    ctiles, tiles = base + offsets[0], base + offsets[1]
+    sums, mean, var = (base + o for o in offsets[2:]) if moments else (None, None, None)
+    _check(lib.sol_pool_kv(k.data_ptr(), _strides(k, indexed), v.data_ptr(), _strides(v, indexed),
+                           _ptr(key_index), _ptr(key_lengths), b, tk, h, d, ctiles, tiles,
+                           sums, mean, var, stream))
+    pooled = {"workspace": ws, "shape": (b, h, d), "ctiles_ptr": ctiles, "tiles_ptr": tiles,
+              "mean_ptr": mean, "var_ptr": var, "cov_ptr": None, "key_tokens": tk,
+              "key_blocks": nkb, "key_lengths": key_lengths}
+    if views:
+        pooled["ctiles"] = _region(ws, offsets[0], torch.bfloat16, (b, h, nct, 2, BLOCK * d))
+        pooled["tiles"] = _region(ws, offsets[1], torch.bfloat16, (b, h, nkb, 2, BLOCK * d))
+        pooled["mean"] = _region(ws, offsets[3], torch.float32, (b, h, d)) if moments else None
+        pooled["var"] = _region(ws, offsets[4], torch.float32, (b, h, d)) if moments else None
+    return pooled
 
 
-def key_covariance(pooled):
+def key_covariance(pooled, stream=None):
     """Adds ``pooled["cov"]``: the full covariance of the key centroids, fp32
     ``[B, H, D, D]`` (``sol_key_covariance``), for the full-covariance
     threshold.  ``pooled`` must come from :func:`pool_kv` with moments."""
-    if pooled["mean"] is None:
+    if pooled["mean_ptr"] is None:
         raise ValueError("the full-covariance threshold needs the key moments (finite beta)")
     lib = library()
-    ctiles = pooled["ctiles"]
-    b, h, _, _, e = ctiles.shape
-    d = e // BLOCK
-    dev = ctiles.device
+    b, h, d = pooled["shape"]
+    dev = pooled["workspace"].device
+    if stream is None:
+        stream = _stream(dev)
     work = torch.empty(lib.sol_key_covariance_workspace_size(b, h, d) // 4, device=dev, dtype=torch.float32)
     cov = torch.empty((b, h, d, d), device=dev, dtype=torch.float32)
-    _check(lib.sol_key_covariance(_ptr(ctiles), _ptr(pooled["mean"]), _ptr(pooled.get("key_lengths")),
-                                  b, pooled["key_tokens"], h, d, _ptr(work), _ptr(cov), _stream(dev)))
+    _check(lib.sol_key_covariance(pooled["ctiles_ptr"], pooled["mean_ptr"], _ptr(pooled["key_lengths"]),
+                                  b, pooled["key_tokens"], h, d, work.data_ptr(), cov.data_ptr(), stream))
     pooled["cov"] = cov
+    pooled["cov_ptr"] = cov.data_ptr()
     return pooled
 
 
@@ -163,47 +201,53 @@ PAIRING = True
 PAIR_MIN_QUERY_BLOCKS = 8192
 
 
-def pair_strides(q, rows=None, min_blocks=None):
+def pair_strides(q, rows=None, min_blocks=None, stream=None):
     """Per-(entry, head) query-block pairing strides (int32 ``[B, H]``), or None
     when pairing does not apply: fewer than ``min_blocks`` query blocks in
     all (by default PAIR_MIN_QUERY_BLOCKS), or a sequence outside the
     library's 4 .. 8192 query blocks."""
-    lib = library()
     indexed = rows is not None
     b, nq = rows.shape if indexed else q.shape[:2]
     h, d = q.shape[-2:]
-    size = lib.sol_pair_workspace_size(b, nq, h, d)
     if min_blocks is None:
         min_blocks = PAIR_MIN_QUERY_BLOCKS
-    if size == 0 or b * h * -(-nq // BLOCK) < min_blocks:
+    if b * h * -(-nq // BLOCK) < min_blocks:
+        return None
+    lib = library()
+    size = lib.sol_pair_workspace_size(b, nq, h, d)
+    if size == 0:
         return None
     q = _rows(q)
+    if stream is None:
+        stream = _stream(q.device)
     work = torch.empty(size // 4, device=q.device, dtype=torch.float32)
     strides = torch.empty((b, h), device=q.device, dtype=torch.int32)
-    _check(lib.sol_pair_strides(_ptr(q), _strides(q, indexed), _ptr(rows), b, nq, h, d,
-                                _ptr(work), _ptr(strides), _stream(q.device)))
+    _check(lib.sol_pair_strides(q.data_ptr(), _strides(q, indexed), _ptr(rows), b, nq, h, d,
+                                work.data_ptr(), strides.data_ptr(), stream))
     return strides
 
 
 def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows=None,
-           debug=False, out=None):
+           debug=False, out=None, stats=True, stream=None):
     """Routing + attention over pooled keys (the ``_sol`` launch of ``kernels.py:218-224``).
 
     ``pooled`` is the dict returned by :func:`pool_kv`.  ``rows`` (indexed
     windows) gathers the query rows.  With ``out`` (a contiguous BF16
     ``[N, H, D]`` tensor, indexed windows only) query i of window w is stored
     at ``out[rows[w, i]]`` instead of into a new ``[W, nq, H, D]`` tensor.
-    Returns ``(out, counts, dbg)``; ``dbg`` is None unless ``debug``.
+    Returns ``(out, counts, dbg)``; ``counts`` is None unless ``stats`` and
+    ``dbg`` is None unless ``debug``.
     """
     lib = library()
     indexed = rows is not None
-    b, h, _, _, e = pooled["tiles"].shape
-    d = e // BLOCK
+    b, h, d = pooled["shape"]
     nkb = pooled["key_blocks"]
     nq = rows.shape[1] if indexed else q.shape[1]
     nk = pooled["key_tokens"]
     q = _rows(q)
     dev = q.device
+    if stream is None:
+        stream = _stream(dev)
     nqb = -(-nq // BLOCK)
     scatter = out is not None
     if scatter:
@@ -213,7 +257,7 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
                              "(indexed windows only)")
     else:
         out = torch.empty((b, nq, h, d), device=dev, dtype=torch.bfloat16)
-    counts = torch.empty((b, nqb, h), device=dev, dtype=torch.int32)
+    counts = torch.empty((b, nqb, h), device=dev, dtype=torch.int32) if stats or debug else None
     dbg = None
     if debug:
         dbg = {"selected": torch.empty((b, nqb, h, nkb), device=dev, dtype=torch.uint8),
@@ -222,15 +266,14 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     prot = None
     if protection is not None:
         prot = protection.contiguous().view(torch.uint8)
-    strides = pair_strides(q, rows) if PAIRING else None
+    strides = pair_strides(q, rows, stream=stream) if PAIRING else None
     _check(lib.sol_attention_fwd(
-        _ptr(q), _strides(q, indexed), _ptr(rows), b, nq, nk, _ptr(pooled.get("key_lengths")), h, d,
-        _ptr(pooled["tiles"]), _ptr(pooled["ctiles"]),
-        _ptr(pooled["mean"]), _ptr(pooled["var"]), _ptr(pooled.get("cov")),
+        q.data_ptr(), _strides(q, indexed), _ptr(rows), b, nq, nk, _ptr(pooled["key_lengths"]), h, d,
+        pooled["tiles_ptr"], pooled["ctiles_ptr"], pooled["mean_ptr"], pooled["var_ptr"], pooled["cov_ptr"],
         _ptr(prot), _ptr(strides), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
-        _ptr(out), _ptr(rows if scatter else None), _ptr(counts),
+        out.data_ptr(), _ptr(rows if scatter else None), _ptr(counts),
         _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
-        _stream(dev)))
+        stream))
     if debug:
         dbg["selected"] = dbg["selected"].bool()
     return out, counts, dbg
@@ -246,14 +289,16 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
     key counts ragged and ``out`` scatters the result rows (see :func:`attend`).
     ``threshold_estimator="full_covariance"`` builds the cutoff from the full
     key covariance (:func:`key_covariance`) instead of its diagonal.
-    Returns ``(out, counts)`` and, with ``debug=True``, a dict of routing
-    diagnostics as a third element.
+    Returns ``(out, counts)`` (``counts`` None unless ``stats``) and, with
+    ``debug=True``, a dict of routing diagnostics as a third element.
     """
-    pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths)
+    stream = _stream(q.device)
+    pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths,
+                     stream=stream, views=debug)
     if threshold_estimator == "full_covariance" and not math.isinf(beta):
-        key_covariance(pooled)
+        key_covariance(pooled, stream)
     out, counts, dbg = attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection, rows,
-                              debug, out)
+                              debug, out, stats, stream)
     if debug:
         dbg.update(pooled)
         return out, counts, dbg
@@ -269,13 +314,14 @@ def plan_protection(rows, keys, key_lengths, local_tokens, ranges):
     """
     lib = library()
     dev = rows.device
+    rows, keys = rows.contiguous(), keys.contiguous()
     w, nq = rows.shape
     nk = keys.shape[1]
     out = torch.empty((w, -(-nq // BLOCK), -(-nk // BLOCK)), device=dev, dtype=torch.uint8)
     rng = torch.tensor(list(ranges), dtype=torch.int64).reshape(-1, 2).to(dev) if ranges else None
-    _check(lib.sol_plan_protection(_ptr(rows.contiguous()), _ptr(keys.contiguous()), _ptr(key_lengths),
+    _check(lib.sol_plan_protection(rows.data_ptr(), keys.data_ptr(), _ptr(key_lengths),
                                    w, nq, nk, int(local_tokens), _ptr(rng),
-                                   0 if rng is None else rng.shape[0], _ptr(out), _stream(dev)))
+                                   0 if rng is None else rng.shape[0], out.data_ptr(), _stream(dev)))
     return out.view(torch.bool)
 
 
@@ -287,7 +333,7 @@ def launch_dense(q, k, v, scale):
     nk = k.shape[1]
     out = torch.empty((b, nq, h, d), device=q.device, dtype=torch.bfloat16)
     tiles = _tiles(b, h, -(-nk // BLOCK), d, q.device)
-    _check(lib.sol_dense_fwd(_ptr(q), _strides(q), _ptr(k), _strides(k), _ptr(v), _strides(v),
-                             b, nq, nk, h, d, float(scale), _ptr(tiles), _ptr(out),
+    _check(lib.sol_dense_fwd(q.data_ptr(), _strides(q), k.data_ptr(), _strides(k), v.data_ptr(), _strides(v),
+                             b, nq, nk, h, d, float(scale), tiles.data_ptr(), out.data_ptr(),
                              _stream(q.device)))
     return out

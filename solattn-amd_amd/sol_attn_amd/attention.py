@@ -33,19 +33,21 @@ class SolStats:
 
 def _validate(q, k, v, scale):
     """Input contract of ``attention.py:19-39``; returns the effective scale."""
-    if any(t.ndim != 4 for t in (q, k, v)):
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
         raise ValueError("Q/K/V must have BTHD rank-4 layout")
     if (k.shape != v.shape or q.shape[0] != k.shape[0]
-            or q.shape[2:] != k.shape[2:] or any(n <= 0 for n in q.shape + k.shape)):
+            or q.shape[2:] != k.shape[2:] or min(q.shape + k.shape) <= 0):
         raise ValueError("Q/K/V batch, head and dimension shapes must agree and be nonempty")
-    if any(t.dtype != torch.bfloat16 for t in (q, k, v)):
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise ValueError("Only BF16 Q/K/V are implemented")
     if q.shape[-1] not in (64, 128):
         raise ValueError("Only head dimensions 64 and 128 are implemented")
-    if any(t.requires_grad for t in (q, k, v)):
+    if q.requires_grad or k.requires_grad or v.requires_grad:
         raise ValueError("Inference only: Q/K/V must not require gradients")
-    if any(t.stride(-1) != 1 or any(s <= 0 for s in t.stride()) for t in (q, k, v)):
-        raise ValueError("Q/K/V need positive strides and contiguous head dimension")
+    for t in (q, k, v):
+        strides = t.stride()
+        if strides[-1] != 1 or min(strides) <= 0:
+            raise ValueError("Q/K/V need positive strides and contiguous head dimension")
     scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     if not math.isfinite(scale) or scale <= 0:
         raise ValueError("scale must be finite and positive")
