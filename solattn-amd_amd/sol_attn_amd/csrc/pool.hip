@@ -21,15 +21,24 @@
 
 namespace sol {
 
-// One wave per SIMD: each wave keeps 16 rows x 16 bytes per lane in flight,
-// so one workgroup per CU already has ~16 MB of reads outstanding chip-wide.
-// More waves only deepen the memory queues: the pass measured 0.50 ms at 3
-// waves per SIMD, 0.47 ms at 2 and 0.42 ms at 1 (same code otherwise).
-template <int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void pool_kv_kernel(PoolParams p) {
+// Two workgroup forms, both covering one 16-block chunk per workgroup:
+// - NW = 4 waves, each pooling 4 blocks in turn (large grids).  One wave per
+//   SIMD: each wave keeps 16 rows x 16 bytes per lane in flight, so one
+//   workgroup per CU already has ~16 MB of reads outstanding chip-wide.  More
+//   waves only deepen the memory queues: the pass measured 0.50 ms at 3 waves
+//   per SIMD, 0.47 ms at 2 and 0.42 ms at 1 (same code otherwise).
+// - NW = 16 / BPI waves, one block (D = 128) or two (D = 64) each, all in
+//   flight at once (grids too small to fill the GPU, where the four
+//   sequential rounds of the first form are the whole run time).
+template <int D, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(1, NW == 4 ? 1 : NW / 4)))
+void pool_kv_kernel(PoolParams p) {
   constexpr int DC = D / 8;          // 16-byte chunks per token row
   constexpr int LPB = DC * 4;        // lanes per key block: 4 chunks of 16 rows
   constexpr int BPI = kWave / LPB;   // key blocks per wave iteration
+  constexpr int NT = NW * kWave;
+  constexpr int ITERS = kPoolChunk / (NW * BPI);  // iterations per wave
+  static_assert(ITERS * NW * BPI == kPoolChunk, "a workgroup covers one chunk");
   using TL = TileLayout<D>;
   __shared__ __align__(16) uint16_t cent[kPoolChunk][D];
 
@@ -47,8 +56,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int nkb = (tk + kBlock - 1) / kBlock;
 
 #pragma unroll
-  for (int it = 0; it < 4 / BPI; ++it) {
-    const int jb = wave * 4 + it * BPI + sub;  // block inside this chunk
+  for (int it = 0; it < ITERS; ++it) {
+    const int jb = (wave * ITERS + it) * BPI + sub;  // block inside this chunk
     const int j = c * kPoolChunk + jb;
     float s[8];
 #pragma unroll
@@ -149,7 +158,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       dst[D + tid] = s2;
     }
   } else {
-    for (int idx = tid; idx < 4 * D; idx += 256) {
+    for (int idx = tid; idx < 4 * D; idx += NT) {
       const int d = idx >> 2, gq = idx & 3;  // 4-centroid group gq of this chunk
       const u32x2 o = {uint32_t(cent[4 * gq][d]) | (uint32_t(cent[4 * gq + 1][d]) << 16),
                        uint32_t(cent[4 * gq + 2][d]) | (uint32_t(cent[4 * gq + 3][d]) << 16)};
@@ -157,6 +166,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   }
 }
+
+// Waves of the wide form: 16 blocks, BPI = 64 / (D / 2) blocks per wave.
+template <int D>
+constexpr int kWideWaves = kPoolChunk / (kWave / (D / 2));
 
 // One workgroup per (batch, head): fold the 16-block chunk sums in torch's
 // cascade order.  The fold is sequential only between 256-block groups: the
@@ -228,12 +241,25 @@ __global__ __launch_bounds__(kMomentThreads) void moments_kernel(const float* __
   var[int64_t(bh) * D + d] = v > 0.f ? v : 0.f;
 }
 
+// Grids of at most this many chunk workgroups (K and V together) use the
+// wide form: they leave most CUs idle, so latency, not bandwidth, sets their
+// time.
+constexpr int64_t kWidePoolGroups = 512;
+
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
   const dim3 grid(unsigned(p.B) * p.H * p.NCHP, 2);
-  if (D == 128)
-    hipLaunchKernelGGL(pool_kv_kernel<128>, grid, dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(pool_kv_kernel<64>, grid, dim3(256), 0, stream, p);
+  const bool wide = 2 * int64_t(p.B) * p.H * p.NCHP <= kWidePoolGroups;
+  if (D == 128) {
+    if (wide)
+      hipLaunchKernelGGL((pool_kv_kernel<128, kWideWaves<128>>), grid, dim3(kWideWaves<128> * kWave), 0, stream, p);
+    else
+      hipLaunchKernelGGL((pool_kv_kernel<128, 4>), grid, dim3(256), 0, stream, p);
+  } else {
+    if (wide)
+      hipLaunchKernelGGL((pool_kv_kernel<64, kWideWaves<64>>), grid, dim3(kWideWaves<64> * kWave), 0, stream, p);
+    else
+      hipLaunchKernelGGL((pool_kv_kernel<64, 4>), grid, dim3(256), 0, stream, p);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || !p.ksum || !p.ctiles) return err;
   if (D == 128)
