@@ -1,6 +1,6 @@
 """CPU oracle for SOL routed attention -- TEST INFRASTRUCTURE ONLY.
 
-This module is the checker, never the product.  Only ``tests/``,
+This module checks the product and is never part of it.  Only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg may import it.
 The shipped package (``sol_attn_amd``) never imports it and has no CPU path.
 
