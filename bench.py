@@ -281,7 +281,7 @@ def main():
                     help="also run a device copy of this many GiB (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
+        print("bench.py measures one GPU only: the library has no multi-GPU path "
               "(heads would shard with no communication); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
