@@ -7,16 +7,21 @@ routing decisions within the stated band, proxies, cutoffs, counts, and the
 outputs under identical routing.  Whole-size properties: the exact-block
 counts equal the decision masks' popcounts (checked on the sample above), a
 repeated call is bit-identical, and beta = -inf equals the dense kernel
-within the BF16 tolerance.
+within the BF16 tolerance.  The same field as 21 frame windows (window f:
+queries frame f, keys frames {0, f-1, f, f+1}, frame 0 protected): one
+ragged call with the fused scatter against the oracle on window 10, and
+bit-identical to a separate call over the windows of 16,128 keys.
 """
 
 import math
 
+import numpy as np
 import pytest
 import torch
 
 import bench
-from sol_attn_amd import dense_attention, sol_attention
+from oracle.sol_oracle import sol_oracle
+from sol_attn_amd import IndexedPlan, dense_attention, sol_attention, sol_attention_indexed
 from sol_testlib import HAS_GPU, assert_close
 from test_kernels import check_routing
 
@@ -52,3 +57,28 @@ def test_full_size_properties(field):
     del a, b
     every = sol_attention(q, k, v, beta=-math.inf)
     assert_close(every.cpu(), dense_attention(q, k, v).cpu())
+
+
+def test_full_size_frame_windows(field):
+    q, k, v = (x[0] for x in field)                       # NHD [84672, 24, 128]
+    tpf = CFG["height"] * CFG["width"]
+    rows, keys = bench.window_plans(CFG["frames"], tpf)
+    prot = dict(protected_ranges=((0, tpf),), local_tokens=64)
+    plan = IndexedPlan.create(rows, keys, q.shape[0], **prot).to("cuda")
+    full = torch.empty_like(q)
+    _, stats = sol_attention_indexed(q, k, v, plan, beta=1.0, return_stats=True, out=full)
+    # Windows 2 .. 18 have 16,128 keys each: their own equal-length plan.
+    mid = list(range(2, CFG["frames"] - 2))
+    sub = IndexedPlan.create(rows[mid], torch.stack([keys[w] for w in mid]), q.shape[0], **prot).to("cuda")
+    part, sub_stats = sol_attention_indexed(q, k, v, sub, beta=1.0, return_stats=True)
+    assert torch.equal(part, full[rows[mid].cuda()])
+    assert torch.equal(sub_stats.exact_blocks, stats.exact_blocks[mid])
+    w, sample = 10, [0, 31, 62]
+    nkb = -(-len(keys[w]) // 64)
+    cpu = [x.cpu() for x in (q, k, v)]
+    ref, counts, _ = sol_oracle(cpu[0][rows[w]][None], cpu[1][keys[w]][None], cpu[2][keys[w]][None], beta=1.0,
+                                local_blocks=-1, protected_blocks=plan.protected_blocks[w:w + 1, :, :nkb].cpu(),
+                                query_blocks=sample)
+    qrows = np.concatenate([np.arange(64 * b, 64 * b + 64) for b in sample])
+    assert_close(full[rows[w][qrows].cuda()].cpu()[None], ref[:, qrows])
+    np.testing.assert_array_equal(stats.exact_blocks[w:w + 1, sample].cpu().numpy(), counts[:, sample])
