@@ -68,22 +68,40 @@ __global__ __launch_bounds__(kMeanThreads) void qblock_means_kernel(PairParams p
   }
 }
 
-// Lag sums of one feature d of one (batch entry, head): thread t holds lag
-// s = t + 1, sum over i of m_i[d] m_{i+s}[d].
-__global__ __launch_bounds__(kMaxLag) void pair_lag_kernel(PairParams p, int D) {
-  __shared__ float x[kMaxPairBlocks];
-  const int d = blockIdx.x, bh = blockIdx.y;
-  const float* src = p.means + (int64_t(bh) * D + d) * p.NQB;
-  for (int i = threadIdx.x; i < p.NQB; i += blockDim.x) x[i] = src[i];
+// Lag sums of one feature d of one (batch entry, head): thread t holds the
+// four lags s = 4 t + 1 .. 4 t + 4, sum over i of m_i[d] m_{i+s}[d].  The
+// thread slides a four-value register window over m_{i+s}, so each step
+// reads m_i (the same for every lane) and one new window value.  The LDS copy
+// is zero-padded past NQB, so terms past the end add exact zeros.
+constexpr int kLagThreads = kMaxLag / 4;
+constexpr int kLagPad = kMaxLag + 4;
+
+__global__ __launch_bounds__(kLagThreads) void pair_lag_kernel(PairParams p, int D) {
+  extern __shared__ float x[];  // NQB + kLagPad floats
+  const int d = blockIdx.x, bh = blockIdx.y, n = p.NQB;
+  const float* src = p.means + (int64_t(bh) * D + d) * n;
+  for (int i = threadIdx.x; i < n + kLagPad; i += kLagThreads) x[i] = i < n ? src[i] : 0.f;
   __syncthreads();
-  const int s = threadIdx.x + 1;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // independent chains
-  int i = 0;
-  for (; i + 3 + s < p.NQB; i += 4)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) acc[u] = fmaf(x[i + u], x[i + u + s], acc[u]);
-  for (; i + s < p.NQB; ++i) acc[0] = fmaf(x[i], x[i + s], acc[0]);
-  p.lags[(int64_t(bh) * D + d) * kMaxLag + threadIdx.x] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  const int s0 = 4 * threadIdx.x + 1;
+  float w0 = x[s0], w1 = x[s0 + 1], w2 = x[s0 + 2], w3 = x[s0 + 3];  // m_{i+s0 .. i+s0+3}, i = 0
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll 4
+  for (int i = 0; i < n; ++i) {
+    const float xi = x[i];
+    a0 = fmaf(xi, w0, a0);
+    a1 = fmaf(xi, w1, a1);
+    a2 = fmaf(xi, w2, a2);
+    a3 = fmaf(xi, w3, a3);
+    w0 = w1;
+    w1 = w2;
+    w2 = w3;
+    w3 = x[i + s0 + 4];
+  }
+  float* dst = p.lags + (int64_t(bh) * D + d) * kMaxLag + 4 * threadIdx.x;
+  dst[0] = a0;
+  dst[1] = a1;
+  dst[2] = a2;
+  dst[3] = a3;
 }
 
 // Per (batch entry, head): mean cosine per lag, pairing score per stride,
@@ -119,7 +137,8 @@ hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream) {
     hipLaunchKernelGGL(qblock_means_kernel<128>, dim3(p.NQB, p.B), dim3(kMeanThreads), 0, stream, p);
   else
     hipLaunchKernelGGL(qblock_means_kernel<64>, dim3(p.NQB, p.B), dim3(kMeanThreads), 0, stream, p);
-  hipLaunchKernelGGL(pair_lag_kernel, dim3(D, p.B * p.H), dim3(kMaxLag), 0, stream, p, D);
+  hipLaunchKernelGGL(pair_lag_kernel, dim3(D, p.B * p.H), dim3(kLagThreads), (p.NQB + kLagPad) * sizeof(float),
+                     stream, p, D);
   hipLaunchKernelGGL(pair_pick_kernel, dim3(p.B * p.H), dim3(kMaxLag), 0, stream, p, D);
   return hipGetLastError();
 }
