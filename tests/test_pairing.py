@@ -73,10 +73,12 @@ def test_no_pairing_below_four_query_blocks():
     assert _native.pair_strides(frames(12, 7).cuda()) is None  # below the default minimum
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("beta", [1.0, -math.inf, 0.0])
-def test_pairing_never_changes_results(beta, monkeypatch):
+def test_pairing_never_changes_results(beta, d, monkeypatch):
     monkeypatch.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)  # pair these 72 query blocks
-    q, k, v = (frames(8, 9, seed=s).cuda() for s in (3, 4, 5))
+    monkeypatch.setenv("SOL_ATTN_GROUP", "2")  # two-block workgroups (this launch is small)
+    q, k, v = (frames(8, 9, d=d, seed=s).cuda() for s in (3, 4, 5))
     ref, ref_stats = sol_attention(q, k, v, beta=beta, kv_sink_tokens=64, return_stats=True)
     monkeypatch.setattr(_native, "PAIRING", False)
     plain, plain_stats = sol_attention(q, k, v, beta=beta, kv_sink_tokens=64, return_stats=True)
@@ -88,13 +90,14 @@ def test_pairing_never_changes_results(beta, monkeypatch):
         monkeypatch.setattr(_native, "pair_strides", lambda q, rows=None, s=s, **kw: torch.full(
             (1, 2), s, device=q.device, dtype=torch.int32))
         monkeypatch.setattr(_native, "PAIRING", True)
-        out, counts, _ = _native.attend(q, pooled, 128 ** -0.5, beta, 1, 64, 0)
+        out, counts, _ = _native.attend(q, pooled, d ** -0.5, beta, 1, 64, 0)
         assert torch.equal(out, ref), s
         assert torch.equal(counts, ref_stats.exact_blocks), s
 
 
 def test_indexed_windows_pair_per_window(monkeypatch):
     monkeypatch.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)
+    monkeypatch.setenv("SOL_ATTN_GROUP", "2")  # two-block workgroups (this launch is small)
     x = [frames(10, 6, seed=s)[0].cuda() for s in (6, 7, 8)]      # [T, H, D] NHD
     t = x[0].shape[0]
     rows = torch.stack((torch.arange(0, t // 2), torch.arange(t // 2, t)))
