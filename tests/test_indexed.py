@@ -73,8 +73,10 @@ def _ragged_case(seed, n=1500, heads=2, d=128):
     return x, rows, keys
 
 
+@pytest.mark.parametrize("group", ["1", "2"])  # one- and two-block workgroups
 @pytest.mark.parametrize("beta", [-math.inf, math.inf, 1.0, 0.0])
-def test_ragged_windows_one_call_equal_separate_calls_and_oracle(beta):
+def test_ragged_windows_one_call_equal_separate_calls_and_oracle(beta, group, monkeypatch):
+    monkeypatch.setenv("SOL_ATTN_GROUP", group)
     x, rows, keys = _ragged_case(11)
     kw = dict(protected_ranges=((0, 7),), local_tokens=64)
     p = IndexedPlan.create(rows, keys, 1500, **kw)
@@ -97,7 +99,9 @@ def test_ragged_windows_one_call_equal_separate_calls_and_oracle(beta):
     assert stats.density() == pytest.approx(float(np.mean(densities)), rel=1e-6)
 
 
-def test_scatter_epilogue_equals_indexed_assignment():
+@pytest.mark.parametrize("group", ["1", "2"])
+def test_scatter_epilogue_equals_indexed_assignment(group, monkeypatch):
+    monkeypatch.setenv("SOL_ATTN_GROUP", group)
     x, rows, keys = _ragged_case(12)
     gpu = [t.cuda() for t in x]
     for plan in (IndexedPlan.create(rows, keys, 1500),
