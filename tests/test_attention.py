@@ -24,11 +24,18 @@ def sdpa(q, k, v):
                                           v.float().cpu().transpose(1, 2)).transpose(1, 2)
 
 
+# Both workgroup forms: one query block per workgroup (what these small
+# launches use by default) and two (what large launches use).
+GROUPS = ["1", "2"]
+
+
+@pytest.mark.parametrize("group", GROUPS)
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("beta", [-math.inf, math.inf, 1.0])
 @pytest.mark.parametrize("strided", [False, True])
-def test_sol_ragged_cross_attention(d, beta, strided):
+def test_sol_ragged_cross_attention(d, beta, strided, group, monkeypatch):
     # test_attention.py:55-69
+    monkeypatch.setenv("SOL_ATTN_GROUP", group)
     q, k, v = tensors(d=d, b=2, device="cuda", strided=strided)
     actual, stats = sol_attention(q, k, v, beta=beta, return_stats=True)
     ref, counts, _ = sol_oracle(q.cpu(), k.cpu(), v.cpu(), beta=beta)
@@ -74,9 +81,12 @@ def test_sol_single_token_no_empty_mass_nan():
         assert torch.equal(sol_attention(q, k, v, beta=beta), v)
 
 
+@pytest.mark.parametrize("group", GROUPS)
 @pytest.mark.parametrize("beta", [-math.inf, math.inf, 1.0])
-def test_sol_multiple_groups_and_tail(beta):
-    # test_attention.py:104-112
+def test_sol_multiple_groups_and_tail(beta, group, monkeypatch):
+    # test_attention.py:104-112; 17 query blocks: the last two-block
+    # workgroup holds one live block.
+    monkeypatch.setenv("SOL_ATTN_GROUP", group)
     q, k, v = tensors(nq=1025, nk=1089, h=1, device="cuda")
     actual, stats = sol_attention(q, k, v, beta=beta, return_stats=True)
     ref, counts, _ = sol_oracle(q.cpu(), k.cpu(), v.cpu(), beta=beta)
