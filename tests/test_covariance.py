@@ -66,7 +66,9 @@ def test_full_covariance_differs_from_diagonal_and_beta_zero_matches():
                            sol_attention(q, k, v, beta=beta, threshold_estimator="full_covariance"))
 
 
-def test_full_covariance_ragged_windows_match_oracle():
+@pytest.mark.parametrize("group", ["1", "2"])  # one- and two-block workgroups
+def test_full_covariance_ragged_windows_match_oracle(group, monkeypatch):
+    monkeypatch.setenv("SOL_ATTN_GROUP", group)
     x = [correlated(1, 3000, 2, 64, s)[0].cuda() for s in (9, 10, 11)]
     rows = torch.stack((torch.arange(0, 700), torch.arange(1500, 2200)))
     keys = [torch.arange(0, 1200), torch.arange(900, 3000)]
