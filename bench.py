@@ -13,13 +13,21 @@ density, the in-house dense HIP kernel, roofline of the dominant kernel
 against the oracle on sampled query blocks, and the oracle's CPU time on that
 sample (extrapolated to the full call).
 
+``--workload NAME`` measures another configuration instead; ``--sweep``
+prints one line per configuration of the parity/measurement table (1,024 x 8
+heads block-smooth; 2 x 4,096 x 16 heads block-smooth and random over beta
+in {-inf, 0, 1, +inf}; 4,096 x 10,000 x 24 heads random cross-attention with
+a head-strided Q).
+
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+    python bench.py --sweep [--no-cpu]
 """
 
 import argparse
 import json
 import math
 import os
+import platform
 import sys
 import time
 
@@ -34,18 +42,35 @@ import torch.nn.functional as F  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "ms/call & dense-equiv TFLOP/s at 84,672 tok H24 D128 BF16; density; err vs oracle"
 
+# Inputs are drawn from ONE generator per workload, seed 0, in the order Q, K,
+# V (block-smooth: each tensor's block centres, then its noise).  The
+# block-smooth and random fixtures use a CPU generator in FP32 and are cast to
+# BF16 before the copy to the GPU, so the oracle and the kernels see the same
+# bits; the 84,672-token field is generated on the GPU (its CPU generation
+# takes about a minute) and copied back for the oracle.
 WORKLOADS = {
     "videodit-84672": dict(batch=1, frames=21, height=48, width=84, heads=24, head_dim=128,
                            beta=1.0, kv_sink_tokens=128, query_sink_tokens=128, local_blocks=1,
                            fixture="smooth-field", seed=0),
-    "selfattn-4096-smooth": dict(batch=2, tokens=4096, heads=16, head_dim=128, beta=1.0,
-                                 kv_sink_tokens=128, query_sink_tokens=128, local_blocks=1,
-                                 fixture="block-smooth", seed=0),
     "selfattn-1024-smooth": dict(batch=1, tokens=1024, heads=8, head_dim=64, beta=1.0,
                                  kv_sink_tokens=128, query_sink_tokens=128, local_blocks=1,
                                  fixture="block-smooth", seed=0),
+    "selfattn-4096-smooth": dict(batch=2, tokens=4096, heads=16, head_dim=128, beta=1.0,
+                                 kv_sink_tokens=128, query_sink_tokens=128, local_blocks=1,
+                                 fixture="block-smooth", seed=0),
+    "selfattn-4096-random": dict(batch=2, tokens=4096, heads=16, head_dim=128, beta=1.0,
+                                 kv_sink_tokens=128, query_sink_tokens=128, local_blocks=1,
+                                 fixture="random", seed=0),
+    "crossattn-4096x10000-random": dict(batch=1, tokens=4096, key_tokens=10000, heads=24, head_dim=128,
+                                        q_head_stride=2, beta=1.0, kv_sink_tokens=64,
+                                        query_sink_tokens=0, local_blocks=0, fixture="random", seed=0),
 }
+SWEEP = (("selfattn-1024-smooth", (1.0,)),
+         ("selfattn-4096-smooth", (-math.inf, 0.0, 1.0, math.inf)),
+         ("selfattn-4096-random", (-math.inf, 0.0, 1.0, math.inf)),
+         ("crossattn-4096x10000-random", (1.0,)))
 
 
 def smooth_field(gen, frames, height, width, heads, dim, device):
@@ -58,20 +83,32 @@ def smooth_field(gen, frames, height, width, heads, dim, device):
     return (tokens + 0.2 * noise).to(torch.bfloat16).contiguous()
 
 
-def block_smooth(gen, batch, tokens, heads, dim, device, noise=0.1):
+def block_smooth(gen, batch, tokens, heads, dim, noise=0.1):
+    """Per 64-token block and head a centre ~N(0,1)^D, plus noise * N(0,1) per token."""
     nb = (tokens + 63) // 64
-    centres = torch.randn((batch, nb, heads, dim), generator=gen, device=device)
+    centres = torch.randn((batch, nb, heads, dim), generator=gen)
     x = centres.repeat_interleave(64, 1)[:, :tokens]
-    return (x + noise * torch.randn(x.shape, generator=gen, device=device)).to(torch.bfloat16)
+    return (x + noise * torch.randn(x.shape, generator=gen)).to(torch.bfloat16)
 
 
 def make_inputs(cfg, device):
-    gen = torch.Generator(device=device).manual_seed(cfg["seed"])
+    """Q, K, V of a workload on `device` (see WORKLOADS for the generators)."""
     if cfg["fixture"] == "smooth-field":
+        gen = torch.Generator(device=device).manual_seed(cfg["seed"])
         return [smooth_field(gen, cfg["frames"], cfg["height"], cfg["width"], cfg["heads"],
                              cfg["head_dim"], device) for _ in range(3)]
-    return [block_smooth(gen, cfg["batch"], cfg["tokens"], cfg["heads"], cfg["head_dim"], device)
-            for _ in range(3)]
+    gen = torch.Generator().manual_seed(cfg["seed"])
+    b, h, d = cfg["batch"], cfg["heads"], cfg["head_dim"]
+    tq = cfg["tokens"]
+    tk = cfg.get("key_tokens", tq)
+    if cfg["fixture"] == "block-smooth":
+        xs = [block_smooth(gen, b, t, h, d) for t in (tq, tk, tk)]
+        return [x.to(device) for x in xs]
+    stride = cfg.get("q_head_stride", 1)
+    q = torch.randn((b, tq, h * stride, d), generator=gen).to(torch.bfloat16)
+    k, v = (torch.randn((b, tk, h, d), generator=gen).to(torch.bfloat16) for _ in range(2))
+    # A head-strided Q: the whole allocation moves to the GPU, the view is taken there.
+    return [q.to(device)[:, :, ::stride], k.to(device), v.to(device)]
 
 
 def event_ms(fn, reps):
@@ -204,16 +241,47 @@ def measured_traffic(workload):
     return None
 
 
-def cpu_baseline(q, k, v, cfg, scale, sample, gpu_out, gpu_sel):
-    """The oracle on `sample` query blocks x all heads, timed on host cores."""
-    from oracle import sol_oracle as orc
+def host_description():
+    """The host the CPU baseline runs on: CPU model, core counts, thread pools."""
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     try:
         from threadpoolctl import threadpool_info
-        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+        blas = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
     except Exception:  # pragma: no cover - informational only
-        threads = os.cpu_count()
+        blas = None
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):  # pragma: no cover
+        affinity = None
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "usable_cpus": affinity,
+            "torch_threads": torch.get_num_threads(), "blas_threads": blas}
+
+
+CPU_BASELINE_KIND = ("NumPy float32 restatement of the reference oracle (oracle/sol_oracle.py): "
+                     "one masked softmax per query block, up to 32 query blocks per vectorised "
+                     "BLAS step; not the reference's torch triple loop")
+
+
+def sample_blocks(nqb, count):
+    """`count` evenly spaced query blocks (all of them when count >= nqb)."""
+    return sorted(set(np.linspace(0, nqb - 1, max(1, min(count, nqb))).round().astype(int).tolist()))
+
+
+def cpu_baseline(q, k, v, cfg, beta, scale, sample, gpu_out, gpu_sel):
+    """The oracle on `sample` query blocks x all heads, timed on host cores;
+    parity of the GPU result on the same sample."""
+    from oracle import sol_oracle as orc
+    host = host_description()
     qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
-    kw = dict(beta=cfg["beta"], scale=scale, local_blocks=cfg["local_blocks"],
+    kw = dict(beta=beta, scale=scale, local_blocks=cfg["local_blocks"],
               kv_sink_tokens=cfg["kv_sink_tokens"], query_sink_tokens=cfg["query_sink_tokens"])
     t0 = time.perf_counter()
     kc = orc.block_means(kn, True)
@@ -225,20 +293,26 @@ def cpu_baseline(q, k, v, cfg, scale, sample, gpu_out, gpu_sel):
     out, counts, info = orc.sol_oracle(qn, kn, vn, query_blocks=sample, **kw)
     t_sample = time.perf_counter() - t0
     nqb = counts.shape[1]
+    whole = len(sample) == nqb
     per_block = max(t_sample - t_setup, 1e-9) / len(sample)
-    t_full = t_setup + per_block * nqb
+    t_full = t_sample if whole else t_setup + per_block * nqb
     rows = np.concatenate([np.arange(64 * x, min(qn.shape[1], 64 * x + 64)) for x in sample])
     got = gpu_out[:, rows].float().cpu().numpy()
     ref = out[:, rows]
     ksel = gpu_sel[:, sample].cpu().numpy()
     osel = info["selected"][:, sample]
-    parity = {"sampled_query_blocks": list(map(int, sample)),
+    parity = {"sampled_query_blocks": "all" if whole else list(map(int, sample)),
               "max_abs": float(np.abs(got - ref).max()),
               "rel_l2": float(np.linalg.norm(got - ref) / np.linalg.norm(ref)),
               "routing_decisions": int(osel.size),
               "routing_mismatches": int((ksel != osel).sum()),
               "counts_equal": bool(np.array_equal(ksel.sum(-1), counts[:, sample]))}
-    return t_full, t_sample, threads, parity
+    heads = q.shape[2]
+    sample_txt = ("the whole call (every query block and head)" if whole else
+                  f"{len(sample)} evenly spaced query blocks x {heads} heads x {q.shape[0]} entries "
+                  f"(all keys, full pooling and moments) in {t_sample:.1f} s; per-query-block cost "
+                  f"extrapolated to {nqb} blocks")
+    return t_full, t_sample, host, parity, sample_txt, whole
 
 
 def threshold_experiment(q, k, v, kw, diag_out, diag_density):
@@ -263,15 +337,134 @@ def threshold_experiment(q, k, v, kw, diag_out, diag_density):
                 "full_covariance": {"ms": full_ms, "density": full_stats.density(), **err(full_out)}}
 
 
+def pool_bytes(b, tk, h, d, nkb, moments):
+    """Algorithmic bytes of the pooling pass (read K and V once; write the K / V
+    block centroids and, with moments, read them back for the mean and
+    variance).  The query means are formed inside the attention kernel from
+    the Q tile it stages anyway, so pooling reads no Q."""
+    reads = 2 * b * tk * h * d * 2
+    writes = b * h * d * nkb * (2 + 2)
+    return reads + writes + (b * nkb * h * d * 2 if moments else 0)
+
+
+def config_record(name, cfg, beta, q, k, v):
+    return {"workload": name, "batch": q.shape[0], "query_tokens": q.shape[1], "key_tokens": k.shape[1],
+            "heads": q.shape[2], "head_dim": q.shape[3], "beta": beta,
+            "kv_sink_tokens": cfg["kv_sink_tokens"], "query_sink_tokens": cfg["query_sink_tokens"],
+            "local_blocks": cfg["local_blocks"], "fixture": cfg["fixture"], "seed": cfg["seed"],
+            "q_head_stride_view": cfg.get("q_head_stride", 1) != 1}
+
+
+def measure(name, cfg, beta, args, dev, headline):
+    """One JSON record: the all-in call, its kernels, the dense control, the
+    roofline of the attention kernel and pooling, parity and the CPU oracle."""
+    from sol_attn_amd import _native, dense_attention, sol_attention
+
+    q, k, v = make_inputs(cfg, dev)
+    b, tq, h, d = q.shape
+    tk = k.shape[1]
+    scale = d ** -0.5
+    kw = dict(beta=beta, local_blocks=cfg["local_blocks"],
+              kv_sink_tokens=cfg["kv_sink_tokens"], query_sink_tokens=cfg["query_sink_tokens"])
+    dense_flops = 4.0 * b * h * tq * tk * d
+    finite = math.isfinite(beta)
+
+    def step():
+        return sol_attention(q, k, v, **kw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    call_ms = event_ms(step, args.steps)
+
+    # Per-kernel breakdown with HIP events on the launch stream.
+    with torch.no_grad():
+        pooled = _native.pool_kv(k, v, moments=finite)
+        reps = max(3, args.steps // 2)
+        pool_ms = event_ms(lambda: _native.pool_kv(k, v, moments=finite), 10)
+        attn_ms = event_ms(lambda: _native.attend(q, pooled, scale, beta, cfg["local_blocks"],
+                                                  cfg["kv_sink_tokens"], cfg["query_sink_tokens"]), reps)
+        ref_out, counts, dbg = _native.attend(q, pooled, scale, beta, cfg["local_blocks"],
+                                              cfg["kv_sink_tokens"], cfg["query_sink_tokens"], debug=True)
+        dense_ms = event_ms(lambda: dense_attention(q, k, v), args.dense_reps)
+    torch.cuda.synchronize()
+    deterministic = bool(torch.equal(ref_out, out))
+    nkb = dbg["selected"].shape[-1]
+    density = counts.float().mean().item() / nkb
+    exact_flops, approx_flops = routing_flops(dbg["selected"], tq, tk, d)
+    attn_tflops = (exact_flops + approx_flops) / (attn_ms * 1e-3) / 1e12
+    pbytes = pool_bytes(b, tk, h, d, nkb, finite)
+    relayout = 2 * b * h * nkb * 64 * d * 2  # the K / V^T tile copy the attention kernels stream
+    traffic = measured_traffic(name)
+    result = {
+        "metric": METRIC,
+        "value": dense_flops / (wall_ms * 1e-3) / 1e12,
+        "unit": "dense-equiv TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall_ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": config_record(name, cfg, beta, q, k, v),
+        "density": density,
+        "deterministic_repeat": deterministic,
+        "sol_ms_per_call_events": call_ms,
+        "kernels_ms": {"pool_kv": pool_ms, "sol_attention": attn_ms, "dense_attention": dense_ms},
+        "dense_hip_ms": dense_ms,
+        "dense_hip_tflops": dense_flops / (dense_ms * 1e-3) / 1e12,
+        "speedup_vs_dense_hip": dense_ms / wall_ms,
+        "roofline": {"bound": "mfma", "achieved": attn_tflops, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": attn_tflops / PEAK_BF16_TFLOPS,
+                     "traffic": traffic["traffic_bytes"] if traffic else None,
+                     "traffic_source": (f"{traffic['source']} ({traffic['kernel']}: rocprofv3 FETCH_SIZE x "
+                                        f"{traffic['fetch_scale']} + WRITE_SIZE x {traffic['write_scale']}, "
+                                        f"scaled by a 1 GiB copy)") if traffic else None,
+                     "kernel": "sol attention (routing + centroid correction + exact blocks)",
+                     "flops_per_launch": exact_flops + approx_flops, "exact_flops": exact_flops,
+                     "exact_only_frac": exact_flops / (attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
+        "pool_roofline": {"bound": "hbm", "achieved": pbytes / (pool_ms * 1e-3) / 1e9,
+                          "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                          "frac": pbytes / (pool_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                          "bytes_per_launch": pbytes,
+                          "bytes_definition": "K and V read once + BF16 K/V centroids written"
+                                              + (" + centroids read for the moments" if finite else ""),
+                          "relayout_bytes_not_counted": relayout,
+                          "with_relayout_frac": (pbytes + relayout) / (pool_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
+    }
+    if headline and finite and not args.no_threshold_experiment:
+        result["threshold_experiment"] = threshold_experiment(q, k, v, kw, out, density)
+    if headline and "frames" in cfg and not args.no_windows:
+        result["indexed_windows"] = bench_windows(q, k, v, cfg, max(3, args.steps // 2), not args.no_cpu)
+    if not args.no_cpu:
+        nqb = -(-tq // 64)
+        sample = list(range(nqb)) if nqb <= 16 else sample_blocks(nqb, args.cpu_blocks if headline else 3)
+        t_full, t_sample, host, parity, sample_txt, whole = cpu_baseline(
+            q, k, v, cfg, beta, scale, sample, out, dbg["selected"])
+        result["cpu_baseline"] = {
+            "value": dense_flops / t_full / 1e12, "unit": "dense-equiv TFLOP/s",
+            "cores": host["blas_threads"] or host["os_cpu_count"], "kind": "port",
+            "implementation": CPU_BASELINE_KIND,
+            "ms_per_call" if whole else "ms_per_call_extrapolated": t_full * 1e3,
+            "sample": sample_txt, "host": host}
+        result["parity_vs_oracle"] = parity
+    return result
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="videodit-84672")
+    ap.add_argument("--beta", type=float, default=None, help="override the workload's beta")
+    ap.add_argument("--sweep", action="store_true",
+                    help="one JSON line per configuration of the parity/measurement table")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-blocks", type=int, default=24,
-                    help="query blocks (evenly spaced, all heads) in the CPU oracle sample")
+                    help="query blocks (evenly spaced, all heads) in the headline CPU oracle sample")
     ap.add_argument("--dense-reps", type=int, default=2)
     ap.add_argument("--no-windows", action="store_true",
                     help="skip the indexed frame-window measurement on the same field")
@@ -285,43 +478,17 @@ def main():
               "(heads would shard with no communication); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
-    from sol_attn_amd import _native, dense_attention, sol_attention
-
-    cfg = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    q, k, v = make_inputs(cfg, dev)
-    b, t, h, d = q.shape
-    scale = d ** -0.5
-    kw = dict(beta=cfg["beta"], local_blocks=cfg["local_blocks"],
-              kv_sink_tokens=cfg["kv_sink_tokens"], query_sink_tokens=cfg["query_sink_tokens"])
-    dense_flops = 4.0 * b * h * t * t * d
-
-    def step():
-        return sol_attention(q, k, v, **kw)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        out = step()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-
-    # Per-kernel breakdown with HIP events on the launch stream.
-    with torch.no_grad():
-        pooled = _native.pool_kv(k, v, moments=True)
-        pool_ms = event_ms(lambda: _native.pool_kv(k, v, moments=False), 10)
-        pool_mom_ms = event_ms(lambda: _native.pool_kv(k, v, moments=True), 10)
-        attn_ms = event_ms(lambda: _native.attend(q, pooled, scale, cfg["beta"], cfg["local_blocks"],
-                                                  cfg["kv_sink_tokens"], cfg["query_sink_tokens"]),
-                           max(3, args.steps // 2))
-        ref_out, counts, dbg = _native.attend(q, pooled, scale, cfg["beta"], cfg["local_blocks"],
-                                              cfg["kv_sink_tokens"], cfg["query_sink_tokens"],
-                                              debug=True)
-        dense_ms = event_ms(lambda: dense_attention(q, k, v), args.dense_reps)
-    torch.cuda.synchronize()
+    if args.sweep:
+        for name, betas in SWEEP:
+            for beta in betas:
+                rec = measure(name, WORKLOADS[name], beta, args, dev, headline=False)
+                print(json.dumps(rec), flush=True)
+        return
+    cfg = WORKLOADS[args.workload]
+    beta = cfg["beta"] if args.beta is None else args.beta
+    result = measure(args.workload, cfg, beta, args, dev, headline=True)
     if args.copy_gib > 0:
         # One elementwise kernel that reads and writes exactly copy_gib GiB each.
         src = torch.empty(int(args.copy_gib * (1 << 30)) // 4, device=dev, dtype=torch.float32)
@@ -330,61 +497,6 @@ def main():
         torch.mul(src, 2.0, out=dst)
         torch.cuda.synchronize()
         del src, dst
-    deterministic = bool(torch.equal(ref_out, out))
-    density = counts.float().mean().item() / dbg["selected"].shape[-1]
-    exact_flops, approx_flops = routing_flops(dbg["selected"], t, t, d)
-    attn_tflops = (exact_flops + approx_flops) / (attn_ms * 1e-3) / 1e12
-    # Algorithmic pooling bytes: read K and V once; write centroids and the K / V^T tiles.
-    pool_bytes = 2 * b * t * h * d * 2 + (pooled["ctiles"].numel() + pooled["tiles"].numel()) * 2
-    pool_gbs = pool_bytes / (pool_ms * 1e-3) / 1e9
-
-    traffic = measured_traffic(args.workload)
-    result = {
-        "metric": "ms/call & dense-equiv TFLOP/s at 84,672 tok H24 D128 BF16; density; err vs oracle",
-        "value": dense_flops / (wall_ms * 1e-3) / 1e12,
-        "unit": "dense-equiv TFLOP/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall_ms,
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": args.workload, "batch": b, "tokens": t, "heads": h, "head_dim": d,
-                   "beta": cfg["beta"], "kv_sink_tokens": cfg["kv_sink_tokens"],
-                   "query_sink_tokens": cfg["query_sink_tokens"], "local_blocks": cfg["local_blocks"],
-                   "fixture": cfg["fixture"], "seed": cfg["seed"]},
-        "density": density,
-        "deterministic_repeat": deterministic,
-        "kernels_ms": {"pool_kv": pool_ms, "pool_kv_moments": pool_mom_ms, "sol_attention": attn_ms,
-                       "dense_attention": dense_ms},
-        "dense_hip_ms": dense_ms,
-        "dense_hip_tflops": dense_flops / (dense_ms * 1e-3) / 1e12,
-        "speedup_vs_dense_hip": dense_ms / wall_ms,
-        "roofline": {"bound": "mfma", "achieved": attn_tflops, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": attn_tflops / PEAK_BF16_TFLOPS,
-                     "traffic": traffic["traffic_bytes"] if traffic else None,
-                     "traffic_source": (f"{traffic['source']} ({traffic['kernel']}: rocprofv3 FETCH_SIZE x "
-                                        f"{traffic['fetch_scale']} + WRITE_SIZE x {traffic['write_scale']}, "
-                                        f"scaled by a 1 GiB copy)") if traffic else None,
-                     "kernel": "sol attention (routing + centroid correction + exact blocks)",
-                     "flops_per_launch": exact_flops + approx_flops, "exact_flops": exact_flops,
-                     "exact_only_frac": exact_flops / (attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS},
-        "pool_roofline": {"bound": "hbm", "achieved": pool_gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                          "frac": pool_gbs / PEAK_HBM_GBS, "bytes_per_launch": pool_bytes},
-    }
-    if not args.no_threshold_experiment:
-        result["threshold_experiment"] = threshold_experiment(q, k, v, kw, out, density)
-    if "frames" in cfg and not args.no_windows:
-        result["indexed_windows"] = bench_windows(q, k, v, cfg, max(3, args.steps // 2), not args.no_cpu)
-    if not args.no_cpu:
-        nqb = (t + 63) // 64
-        sample = sorted(set(np.linspace(0, nqb - 1, max(1, min(args.cpu_blocks, nqb))).round().astype(int).tolist()))
-        t_full, t_sample, threads, parity = cpu_baseline(q, k, v, cfg, scale, sample, out,
-                                                         dbg["selected"])
-        result["cpu_baseline"] = {
-            "value": dense_flops / t_full / 1e12, "unit": "dense-equiv TFLOP/s", "cores": threads,
-            "kind": "port", "ms_per_call_extrapolated": t_full * 1e3,
-            "sample": (f"oracle on {len(sample)} evenly spaced query blocks x {h} heads (all keys, "
-                       f"full pooling and moments) in {t_sample:.1f} s; per-query-block cost "
-                       f"extrapolated to {nqb} blocks")}
-        result["parity_vs_oracle"] = parity
     print(json.dumps(result), flush=True)
 
 

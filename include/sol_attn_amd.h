@@ -12,7 +12,11 @@
  *    operand takes three element strides {batch, token, head}.  When an index
  *    pointer ([batch, tokens] int64, device memory) is given, token t of
  *    batch b is row index[b * tokens + t] and the batch stride is ignored
- *    (indexed windows, indexed.py:99).
+ *    (indexed windows, indexed.py:99).  sequence_length is then the number
+ *    of rows the index may address: the caller validates its indices (as
+ *    IndexedPlan.create does), and an entry outside [0, sequence_length) --
+ *    a plan changed after validation -- is clamped into that range, so every
+ *    access stays inside the caller's tensors.
  *  - Ragged indexed windows: key_lengths (int32 [batch], device memory; NULL =
  *    every entry has key_tokens keys) gives entry b's key count, 1..key_tokens;
  *    its keys are the first key_lengths[b] rows of its key_index row, and every
@@ -37,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 5
+#define SOL_ABI_VERSION 6
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
 
@@ -70,6 +74,7 @@ int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t hea
 /* K/V block pooling, attention tiles and diagonal key moments, in one pass over
  * K and V.  Replaces `_pooled(k)`, `_pooled(v)` (kernels.py:185-190, kernel
  * `_pool` kernels.py:16-27) and `_moments` (kernels.py:30-49).
+ * sequence_length: rows key_index may address (ignored without key_index).
  * ctiles receives the BF16 (round-to-nearest-even) 64-token block means of K
  * and V (NULL: tiles only); tiles receives every key block as the tile pair the
  * attention kernels stream; when key_mean/key_var/chunk_sums are all
@@ -78,8 +83,8 @@ int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t hea
 int sol_pool_kv(const void* k, const int64_t* k_strides,
                 const void* v, const int64_t* v_strides,
                 const int64_t* key_index, const int32_t* key_lengths,
-                int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
-                void* ctiles, void* tiles,
+                int64_t sequence_length, int64_t batch, int64_t key_tokens,
+                int64_t heads, int64_t head_dim, void* ctiles, void* tiles,
                 float* chunk_sums, float* key_mean, float* key_var,
                 void* stream);
 
@@ -102,8 +107,9 @@ int64_t sol_pair_workspace_size(int64_t batch, int64_t query_tokens, int64_t hea
  * schedule.  No counterpart in the reference (one Triton program per query
  * block, no pairing). */
 int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* query_index,
-                     int64_t batch, int64_t query_tokens, int64_t heads, int64_t head_dim,
-                     void* workspace, int32_t* strides, void* stream);
+                     int64_t sequence_length, int64_t batch, int64_t query_tokens,
+                     int64_t heads, int64_t head_dim, void* workspace, int32_t* strides,
+                     void* stream);
 
 /* Workspace bytes of sol_key_covariance (0: unsupported shape). */
 int64_t sol_key_covariance_workspace_size(int64_t batch, int64_t heads, int64_t head_dim);
@@ -135,13 +141,19 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
  * out_index (int64 [batch, query_tokens], device) is given, a contiguous BF16
  * [N, heads, head_dim] whose row out_index[b * query_tokens + t] receives
  * query t of entry b (the scatter `out[rows] = result` of a window adapter,
- * integrations/vdn.py:67-74, fused into the store; rows must be distinct).
+ * integrations/vdn.py:67-74, fused into the store; rows must be distinct;
+ * rows outside [0, sequence_length) are not stored).  sequence_length: the
+ * rows query_index may address and out_index's N (ignored without either).
  * counts: NULL or int32 [batch, NQB, heads] exact-block counts.
  * debug_selected (uint8) / debug_proxy (fp32): NULL or [batch, NQB, heads, NKB]
  * routing decisions and proxies (natural-log units); debug_cutoff: NULL or
- * fp32 [batch, NQB, heads].  Debug outputs are for verification, not timing. */
+ * fp32 [batch, NQB, heads].  Debug outputs are for verification, not timing.
+ * workgroup_form: 0 picks the schedule by launch size; 1 or 2 forces one or
+ * two query blocks per workgroup (both give bit-identical results; tests run
+ * both).  No counterpart in the reference (one Triton program per query
+ * block). */
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
-                      int64_t batch, int64_t query_tokens, int64_t key_tokens,
+                      int64_t sequence_length, int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,
                       const void* tiles, const void* ctiles,
                       const float* key_mean, const float* key_var, const float* key_cov,
@@ -150,7 +162,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
-                      void* stream);
+                      int workgroup_form, void* stream);
 
 /* Packed-block protection of indexed windows, built on the GPU: the
  * protection part of `IndexedPlan.create` (indexed.py:27-62).  Block (w, qb,

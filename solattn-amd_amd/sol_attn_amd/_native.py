@@ -16,8 +16,7 @@ import os
 import torch
 
 BLOCK = 64
-MAX_KEY_BLOCKS = 8192
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -27,19 +26,20 @@ _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _dbl = ctypes.c_double
+_int = ctypes.c_int
 
 _SIGNATURES = {
     "sol_abi_version": ([], ctypes.c_int),
     "sol_last_error": ([], ctypes.c_char_p),
     "sol_pool_sizes": ([_i64, _i64, _i64, _i64, _i64p], ctypes.c_int),
-    "sol_pool_kv": ([_p, _i64p, _p, _i64p, _p, _p, _i64, _i64, _i64, _i64,
+    "sol_pool_kv": ([_p, _i64p, _p, _i64p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                      _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_pair_workspace_size": ([_i64, _i64, _i64, _i64], ctypes.c_int64),
-    "sol_pair_strides": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
-    "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _p, _i64, _i64,
+    "sol_pair_strides": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64,
                            _p, _p, _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
-                           _p, _p, _p, _p, _p, _p, _p], ctypes.c_int),
+                           _p, _p, _p, _p, _p, _p, _int, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
                        _dbl, _p, _p, _p], ctypes.c_int),
     "sol_plan_protection": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
@@ -159,8 +159,8 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None, stream=None, v
     ctiles, tiles = base + offsets[0], base + offsets[1]
     sums, mean, var = (base + o for o in offsets[2:]) if moments else (None, None, None)
     _check(lib.sol_pool_kv(k.data_ptr(), _strides(k, indexed), v.data_ptr(), _strides(v, indexed),
-                           _ptr(key_index), _ptr(key_lengths), b, tk, h, d, ctiles, tiles,
-                           sums, mean, var, stream))
+                           _ptr(key_index), _ptr(key_lengths), k.shape[0] if indexed else 0,
+                           b, tk, h, d, ctiles, tiles, sums, mean, var, stream))
     pooled = {"workspace": ws, "shape": (b, h, d), "ctiles_ptr": ctiles, "tiles_ptr": tiles,
               "mean_ptr": mean, "var_ptr": var, "cov_ptr": None, "key_tokens": tk,
               "key_blocks": nkb, "key_lengths": key_lengths}
@@ -192,6 +192,10 @@ def key_covariance(pooled, stream=None):
     return pooled
 
 
+# Query blocks per SOL workgroup: 0 lets the library choose by launch size;
+# 1 or 2 forces a form (results are bit-identical; the tests run both).
+WORKGROUP_FORM = 0
+
 # Pair query blocks by the stride sol_pair_strides picks (False: adjacent
 # blocks share a workgroup).  Results are identical either way.
 PAIRING = True
@@ -222,7 +226,8 @@ def pair_strides(q, rows=None, min_blocks=None, stream=None):
         stream = _stream(q.device)
     work = torch.empty(size // 4, device=q.device, dtype=torch.float32)
     strides = torch.empty((b, h), device=q.device, dtype=torch.int32)
-    _check(lib.sol_pair_strides(q.data_ptr(), _strides(q, indexed), _ptr(rows), b, nq, h, d,
+    _check(lib.sol_pair_strides(q.data_ptr(), _strides(q, indexed), _ptr(rows),
+                                q.shape[0] if indexed else 0, b, nq, h, d,
                                 work.data_ptr(), strides.data_ptr(), stream))
     return strides
 
@@ -268,12 +273,13 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
         prot = protection.contiguous().view(torch.uint8)
     strides = pair_strides(q, rows, stream=stream) if PAIRING else None
     _check(lib.sol_attention_fwd(
-        q.data_ptr(), _strides(q, indexed), _ptr(rows), b, nq, nk, _ptr(pooled["key_lengths"]), h, d,
+        q.data_ptr(), _strides(q, indexed), _ptr(rows), q.shape[0] if indexed else 0,
+        b, nq, nk, _ptr(pooled["key_lengths"]), h, d,
         pooled["tiles_ptr"], pooled["ctiles_ptr"], pooled["mean_ptr"], pooled["var_ptr"], pooled["cov_ptr"],
         _ptr(prot), _ptr(strides), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
         out.data_ptr(), _ptr(rows if scatter else None), _ptr(counts),
         _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
-        stream))
+        WORKGROUP_FORM, stream))
     if debug:
         dbg["selected"] = dbg["selected"].bool()
     return out, counts, dbg

@@ -57,6 +57,17 @@ def _validate(q, k, v, scale):
     return scale
 
 
+# Key blocks one call can route: the routing bitmask of each query block lives
+# in LDS (SOL_MAX_KEY_BLOCKS in include/sol_attn_amd.h).
+MAX_KEY_TOKENS = 8192 * 64
+
+
+def _key_length(tokens):
+    """Rejects key sequences beyond the routing bitmask before any launch."""
+    if tokens > MAX_KEY_TOKENS:
+        raise ValueError(f"Key sequences longer than {MAX_KEY_TOKENS} tokens are not supported")
+
+
 def _nonnegative_integer(name, value):
     if not isinstance(value, int) or isinstance(value, bool) or value < 0:
         raise ValueError(f"{name} must be a nonnegative integer")
@@ -112,6 +123,7 @@ def sol_attention(q, k, v, *, beta=1.0, scale=None, local_blocks=1,
         _nonnegative_integer(name, value)
     if kv_sink_tokens > k.shape[1] or query_sink_tokens > q.shape[1]:
         raise ValueError("Sink token counts must not exceed their sequence lengths")
+    _key_length(k.shape[1])
     from ._native import launch_sol
     with torch.no_grad(), torch.cuda.device(q.device):
         out, counts = launch_sol(q, k, v, scale, beta, local_blocks,

@@ -28,7 +28,6 @@
 // The dense control streams every exact tile, 128 queries per workgroup
 // (4 waves x 32 queries, full 64-key tiles per wave).
 #include <algorithm>
-#include <cstdlib>
 
 #include "sol_device.h"
 #include "sol_internal.h"
@@ -479,7 +478,11 @@ __device__ __forceinline__ void store_output(const AttnParams& p, int b, int h, 
   using S = Shape<D>;
   const float den = pair_sum(st.den);
   if (t >= p.Tq) return;
-  const int64_t row = p.out_index ? p.out_index[int64_t(b) * p.Tq + t] : int64_t(b) * p.Tq + t;
+  int64_t row = int64_t(b) * p.Tq + t;
+  if (p.out_index) {
+    row = p.out_index[row];
+    if (row < 0 || row >= p.out_rows) return;  // outside the output: not stored
+  }
   uint16_t* orow = p.out + (row * p.H + h) * D;
 #pragma unroll
   for (int dt = 0; dt < S::DT; ++dt)
@@ -948,8 +951,8 @@ constexpr int kSolRing = 2;
 // 2 workgroups): such launches run one query block per workgroup instead,
 // which doubles the workgroups and has no union to stream.  Both forms give
 // bit-identical results (a wave's tiles, their order and its softmax state
-// do not depend on its partner).  SOL_ATTN_GROUP=1 or 2 in the environment
-// forces one form (for tests and tuning).
+// do not depend on its partner).  AttnParams::workgroup_form 1 or 2 forces
+// one form (tests run both).
 constexpr int64_t kSmallLaunchGroups = 512;
 
 template <int D, int G>
@@ -962,7 +965,7 @@ void launch_sol_group(const AttnParams& p, hipStream_t stream) {
 
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
   int g = int64_t(p.B) * p.H * ((p.NQB + 1) / 2) < kSmallLaunchGroups ? 1 : 2;
-  if (const char* forced = std::getenv("SOL_ATTN_GROUP")) g = std::atoi(forced) == 1 ? 1 : 2;
+  if (p.workgroup_form == 1 || p.workgroup_form == 2) g = p.workgroup_form;
   if (D == 128) {
     if (g == 1) launch_sol_group<128, 1>(p, stream); else launch_sol_group<128, 2>(p, stream);
   } else {

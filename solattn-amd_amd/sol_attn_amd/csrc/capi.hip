@@ -41,10 +41,13 @@ bool shape_ok(int64_t batch, int64_t tokens, int64_t heads, int64_t head_dim) {
          batch * heads < (int64_t(1) << 24) && tokens < (int64_t(1) << 30);
 }
 
-sol::TokenRows rows_of(const void* base, const int64_t* strides, const int64_t* index, int64_t tokens) {
+// `rows`: rows an index entry may address (indexed sources; clamped into it).
+sol::TokenRows rows_of(const void* base, const int64_t* strides, const int64_t* index, int64_t tokens,
+                       int64_t rows = 1) {
   sol::TokenRows r;
   r.base = static_cast<const uint16_t*>(base);
   r.index = index;
+  r.N = rows;
   r.sb = strides[0];
   r.st = strides[1];
   r.sh = strides[2];
@@ -78,8 +81,8 @@ namespace {
 
 int pool_checked(const char* who, const void* k, const int64_t* k_strides, const void* v,
                  const int64_t* v_strides, const int64_t* key_index, const int32_t* key_lengths,
-                 int64_t batch,
-                 int64_t key_tokens, int64_t heads, int64_t head_dim, void* ctiles, void* tiles,
+                 int64_t sequence_length, int64_t batch, int64_t key_tokens, int64_t heads,
+                 int64_t head_dim, void* ctiles, void* tiles,
                  float* chunk_sums, float* key_mean, float* key_var, void* stream) {
   static thread_local std::string msg;
   auto err = [&](int code, const char* what) {
@@ -91,6 +94,8 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
   const bool indexed = key_index != nullptr;
   if (!operand_ok(k, k_strides, indexed) || !operand_ok(v, v_strides, indexed))
     return err(SOL_ERR_INVALID, "K/V need 16-byte aligned rows and positive strides");
+  if (indexed && sequence_length <= 0)
+    return err(SOL_ERR_INVALID, "an indexed source needs sequence_length > 0");
   if (!ctiles && !tiles) return err(SOL_ERR_INVALID, "nothing to write");
   if ((ctiles && !aligned16(ctiles)) || (tiles && !aligned16(tiles)))
     return err(SOL_ERR_INVALID, "ctiles/tiles must be 16-byte aligned device buffers");
@@ -100,8 +105,8 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
   if (nkb > (int64_t(1) << 19)) return err(SOL_ERR_UNSUPPORTED, "too many key blocks");
   sol::PoolParams p;
-  p.k = rows_of(k, k_strides, key_index, key_tokens);
-  p.v = rows_of(v, v_strides, key_index, key_tokens);
+  p.k = rows_of(k, k_strides, key_index, key_tokens, sequence_length);
+  p.v = rows_of(v, v_strides, key_index, key_tokens, sequence_length);
   p.klen = key_lengths;
   p.ctiles = static_cast<uint16_t*>(ctiles);
   p.tiles = static_cast<uint16_t*>(tiles);
@@ -120,12 +125,12 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
 }  // namespace
 
 int sol_pool_kv(const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
-                const int64_t* key_index, const int32_t* key_lengths, int64_t batch,
-                int64_t key_tokens, int64_t heads, int64_t head_dim, void* ctiles, void* tiles,
-                float* chunk_sums, float* key_mean, float* key_var, void* stream) {
-  return pool_checked("sol_pool_kv", k, k_strides, v, v_strides, key_index, key_lengths, batch,
-                      key_tokens, heads, head_dim, ctiles, tiles, chunk_sums, key_mean, key_var,
-                      stream);
+                const int64_t* key_index, const int32_t* key_lengths, int64_t sequence_length,
+                int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim, void* ctiles,
+                void* tiles, float* chunk_sums, float* key_mean, float* key_var, void* stream) {
+  return pool_checked("sol_pool_kv", k, k_strides, v, v_strides, key_index, key_lengths,
+                      sequence_length, batch, key_tokens, heads, head_dim, ctiles, tiles,
+                      chunk_sums, key_mean, key_var, stream);
 }
 
 int64_t sol_pair_workspace_size(int64_t batch, int64_t query_tokens, int64_t heads, int64_t head_dim) {
@@ -136,8 +141,9 @@ int64_t sol_pair_workspace_size(int64_t batch, int64_t query_tokens, int64_t hea
 }
 
 int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* query_index,
-                     int64_t batch, int64_t query_tokens, int64_t heads, int64_t head_dim,
-                     void* workspace, int32_t* strides, void* stream) {
+                     int64_t sequence_length, int64_t batch, int64_t query_tokens,
+                     int64_t heads, int64_t head_dim, void* workspace, int32_t* strides,
+                     void* stream) {
   const int64_t bytes = sol_pair_workspace_size(batch, query_tokens, heads, head_dim);
   if (bytes == 0)
     return fail(SOL_ERR_UNSUPPORTED,
@@ -146,8 +152,10 @@ int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* que
     return fail(SOL_ERR_INVALID, "sol_pair_strides: Q needs 16-byte aligned rows and positive strides");
   if (!workspace || !strides || !aligned16(workspace))
     return fail(SOL_ERR_INVALID, "sol_pair_strides: workspace (16-byte aligned) and strides are required");
+  if (query_index && sequence_length <= 0)
+    return fail(SOL_ERR_INVALID, "sol_pair_strides: an indexed Q needs sequence_length > 0");
   sol::PairParams p;
-  p.q = rows_of(q, q_strides, query_index, query_tokens);
+  p.q = rows_of(q, q_strides, query_index, query_tokens, sequence_length);
   p.B = int(batch);
   p.H = int(heads);
   p.Tq = int(query_tokens);
@@ -214,7 +222,8 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
 }
 
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
-                      int64_t batch, int64_t query_tokens, int64_t key_tokens,
+                      int64_t sequence_length, int64_t batch, int64_t query_tokens,
+                      int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,
                       const void* tiles, const void* ctiles, const float* key_mean,
                       const float* key_var, const float* key_cov, const uint8_t* protection,
@@ -222,12 +231,16 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
-                      void* stream) {
+                      int workgroup_form, void* stream) {
   if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
       key_tokens >= (int64_t(1) << 30))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: unsupported shape (head_dim must be 64 or 128)");
   if (!operand_ok(q, q_strides, query_index != nullptr))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: Q needs 16-byte aligned rows and positive strides");
+  if ((query_index || out_index) && sequence_length <= 0)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_index / out_index need sequence_length > 0");
+  if (workgroup_form < 0 || workgroup_form > 2)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: workgroup_form must be 0, 1 or 2");
   if (!std::isfinite(scale) || scale <= 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: scale must be finite and positive");
   if (std::isnan(beta)) return fail(SOL_ERR_INVALID, "sol_attention_fwd: beta must not be NaN");
@@ -246,10 +259,12 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
     return fail(SOL_ERR_UNSUPPORTED, "sol_attention_fwd: grid too large");
   sol::AttnParams p;
   std::memset(&p, 0, sizeof(p));
-  p.q = rows_of(q, q_strides, query_index, query_tokens);
+  p.q = rows_of(q, q_strides, query_index, query_tokens, sequence_length);
   p.pair_stride = pair_strides;
   p.klen = key_lengths;
   p.out_index = out_index;
+  p.out_rows = sequence_length;
+  p.workgroup_form = workgroup_form;
   p.tiles = static_cast<const uint16_t*>(tiles);
   p.ctiles = static_cast<const uint16_t*>(ctiles);
   p.mean = key_mean;
@@ -293,7 +308,7 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
   if (!out || !aligned16(out)) return fail(SOL_ERR_INVALID, "sol_dense_fwd: out must be 16-byte aligned");
   if (batch * heads * cdiv(query_tokens, 128) >= (int64_t(1) << 31))
     return fail(SOL_ERR_UNSUPPORTED, "sol_dense_fwd: grid too large");
-  const int rc = pool_checked("sol_dense_fwd", k, k_strides, v, v_strides, nullptr, nullptr, batch,
+  const int rc = pool_checked("sol_dense_fwd", k, k_strides, v, v_strides, nullptr, nullptr, 0, batch,
                               key_tokens, heads, head_dim, nullptr, tiles, nullptr, nullptr,
                               nullptr, stream);
   if (rc != SOL_OK) return rc;

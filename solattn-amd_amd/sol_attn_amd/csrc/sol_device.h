@@ -71,14 +71,19 @@ __device__ __forceinline__ u32x4 zero_u32x4() {
 
 // Row of one attention operand: token t of batch b, head h.  Either strided
 // BTHD addressing or (indexed windows) a gather through an int64 token index.
+// An index entry outside [0, N) (a plan whose index tensors were changed
+// after validation) is clamped into the source, so that every gather stays
+// inside the caller's tensor whatever the index holds.
 struct TokenRows {
   const uint16_t* base;
   const int64_t* index;  // nullable; [B, T] original token ids
   int64_t sb, st, sh;    // element strides (batch ignored when indexed)
+  int64_t N;             // rows an index entry may address (indexed sources)
   int T;
 
+  __device__ __forceinline__ int64_t clamp_row(int64_t r) const { return min(max(r, int64_t(0)), N - 1); }
   __device__ __forceinline__ const uint16_t* row(int b, int t, int h) const {
-    if (index) return base + index[int64_t(b) * T + t] * st + int64_t(h) * sh;
+    if (index) return base + clamp_row(index[int64_t(b) * T + t]) * st + int64_t(h) * sh;
     return base + int64_t(b) * sb + int64_t(t) * st + int64_t(h) * sh;
   }
 };
@@ -106,7 +111,7 @@ __device__ __forceinline__ void load_rows16(const TokenRows& r, int b, int t0, i
     const int64_t* idx = r.index + int64_t(b) * r.T;
     int64_t row[N];
 #pragma unroll
-    for (int i = 0; i < N; ++i) row[i] = idx[min(t0 + i, t_last)];
+    for (int i = 0; i < N; ++i) row[i] = r.clamp_row(idx[min(t0 + i, t_last)]);
 #pragma unroll
     for (int i = 0; i < N; ++i) p[i] = r.base + row[i] * r.st + int64_t(h) * r.sh + col;
   } else {

@@ -58,6 +58,7 @@ struct AttnParams {
   const int32_t* pair_stride;  // [B, H] query-block pairing stride, or null: adjacent pairs
   const int32_t* klen;         // [B] key tokens per batch entry (<= Tk), or null: all Tk
   const int64_t* out_index;    // [B, Tq] output rows of an [N, H, D] output, or null
+  int64_t out_rows;            // N: rows of an out_index output (others are skipped)
   const uint16_t* tiles;       // [B, H, NKB, 2, 64 * D] from the pooling pass
   const uint16_t* ctiles;      // [B, H, NCT, 2, 64 * D] centroid tiles
   const float* mean;           // [B, H, D]
@@ -74,6 +75,7 @@ struct AttnParams {
   int force;          // 0 finite beta, 1 beta = -inf (all exact), 2 beta = +inf
   int local_blocks;   // < 0 disables the local band
   int kv_sink_blocks, q_sink_blocks;
+  int workgroup_form;  // 0: by launch size; 1 / 2: query blocks per SOL workgroup
 };
 
 // Indexed-window protection (plan.hip).

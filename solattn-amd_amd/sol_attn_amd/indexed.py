@@ -18,7 +18,7 @@ import math
 
 import torch
 
-from .attention import SolStats, _validate, _nonnegative_integer, _threshold_estimator
+from .attention import SolStats, _key_length, _validate, _nonnegative_integer, _threshold_estimator
 
 BLOCK = 64
 
@@ -41,6 +41,12 @@ def _touches(keys, lo, hi_inclusive, lengths):
     val = torch.gather(keys[:, None, :].expand(-1, pos.shape[1], -1), 2,
                        pos.clamp(max=nk - 1))
     return inside & (val <= hi_inclusive[..., None])
+
+
+def _distinct(rows):
+    """No row index appears twice in the plan (rows are sorted per window, so
+    only different windows can share one)."""
+    return bool(torch.unique(rows).numel() == rows.numel())
 
 
 def _index_matrix(name, x, sequence_length, device=torch.device("cpu")):
@@ -71,6 +77,9 @@ class IndexedPlan:
     protected_blocks: torch.Tensor
     sequence_length: int
     key_lengths: "torch.Tensor | None" = None  # int32 [W] for ragged windows, else None
+    # Whether no query row appears in two windows (set by create(); None for a
+    # plan built directly, checked on first use with out=).
+    rows_distinct: "bool | None" = None
 
     @classmethod
     def create(cls, rows, keys, sequence_length, *, protected_ranges=(), local_tokens=64):
@@ -119,12 +128,13 @@ class IndexedPlan:
                 raise ValueError("Invalid protected key range")
         rows = rows.clone().contiguous()
         keys = padded.clone().contiguous()
+        distinct = _distinct(rows)
         if dev.type == "cuda":
             from ._native import plan_protection
             key_lengths = lengths.to(torch.int32).to(dev) if ragged else None
             with torch.cuda.device(dev):
                 protection = plan_protection(rows, keys, key_lengths, local_tokens, ranges)
-            return cls(rows, keys, protection, sequence_length, key_lengths)
+            return cls(rows, keys, protection, sequence_length, key_lengths, distinct)
         w, nq = rows.shape
         nqb = (nq + BLOCK - 1) // BLOCK
         first = rows[:, ::BLOCK]                                        # [W, NQB]
@@ -135,12 +145,13 @@ class IndexedPlan:
             hi = torch.full((w, 1), b - 1, dtype=torch.int64)
             protection |= _touches(keys, lo, hi, lengths)
         return cls(rows, keys, protection.contiguous(), sequence_length,
-                   lengths.to(torch.int32) if ragged else None)
+                   lengths.to(torch.int32) if ragged else None, distinct)
 
     def to(self, device):
         return IndexedPlan(self.rows.to(device), self.keys.to(device),
                            self.protected_blocks.to(device), self.sequence_length,
-                           None if self.key_lengths is None else self.key_lengths.to(device))
+                           None if self.key_lengths is None else self.key_lengths.to(device),
+                           self.rows_distinct)
 
 
 def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=False, out=None,
@@ -157,7 +168,10 @@ def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=F
     stored directly at ``out[plan.rows[w, i]]`` -- the ``out[rows] = result``
     step of a window adapter fused into the kernel's store -- and ``out`` is
     returned; other rows of ``out`` are left as they were.  Rows shared by
-    two windows of one plan would race, so a plan's rows must be distinct.
+    two windows of one plan would race, so ``out=`` is rejected for such a
+    plan.  The kernels clamp index entries into the sequence and skip output
+    rows outside it, so a plan whose tensors were changed after ``create``
+    cannot make them access memory outside Q/K/V or ``out``.
 
     ``threshold_estimator``: as in :func:`sol_attention`.
     """
@@ -185,6 +199,10 @@ def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=F
     if out is not None and (out.dtype != torch.bfloat16 or out.shape != q.shape
                             or not out.is_contiguous() or out.device != q.device):
         raise ValueError("out must be a contiguous BF16 tensor shaped like Q on its device")
+    if out is not None and not (plan.rows_distinct if plan.rows_distinct is not None
+                                else _distinct(plan.rows)):
+        raise ValueError("out= needs a plan whose windows share no query row")
+    _key_length(plan.keys.shape[1])
     beta = float(beta)
     if math.isnan(beta):
         raise ValueError("beta must not be NaN")

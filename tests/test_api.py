@@ -106,6 +106,23 @@ def test_indexed_api_rejects_cpu_inputs():
         sol_attention_indexed(x, x[:10], x, p)
 
 
+def test_plan_records_whether_windows_share_rows():
+    keys = torch.arange(100).reshape(1, -1).expand(2, -1).contiguous()
+    apart = IndexedPlan.create(torch.tensor([[1, 2], [3, 4]]), keys, 200)
+    shared = IndexedPlan.create(torch.tensor([[1, 2], [2, 4]]), keys, 200)
+    assert apart.rows_distinct is True and apart.to("cpu").rows_distinct is True
+    assert shared.rows_distinct is False and shared.to("cpu").rows_distinct is False
+    direct = IndexedPlan(apart.rows, apart.keys, apart.protected_blocks, 200)
+    assert direct.rows_distinct is None  # checked on first use with out=
+
+
+def test_key_length_cap_is_a_value_error():
+    from sol_attn_amd import attention
+    attention._key_length(attention.MAX_KEY_TOKENS)
+    with pytest.raises(ValueError, match="Key sequences longer than 524288 tokens"):
+        attention._key_length(attention.MAX_KEY_TOKENS + 1)
+
+
 def test_stats_density():
     s = SolStats(torch.tensor([[[2, 4]]], dtype=torch.int32), 4)
     assert s.density() == 0.75
@@ -127,7 +144,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == 5
+    assert native.sol_abi_version() == 6
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -149,21 +166,31 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     rc = native.sol_dense_fwd(fake, strides, fake, strides, fake, strides, 1, 193, 317, 2, 64,
                               float("nan"), fake, fake, None)
     assert rc == -1 and b"scale" in native.sol_last_error()
-    rc = native.sol_attention_fwd(fake, strides, None, 1, 193, 317, None, 2, 64, fake, fake,
+    attn = lambda index, n, form: native.sol_attention_fwd(  # noqa: E731
+        fake, strides, index, n, 1, 193, 317, None, 2, 64, fake, fake, fake, fake, None, None, None,
+        0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, form, None)
+    rc = native.sol_attention_fwd(fake, strides, None, 0, 1, 193, 317, None, 2, 64, fake, fake,
                                   None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None,
-                                  None, None, None, None)
+                                  None, None, None, 0, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
-    rc = native.sol_pair_strides(fake, strides, None, 1, 192, 2, 64, fake, fake, None)
+    assert attn(None, 0, 3) == -1 and b"workgroup_form" in native.sol_last_error()
+    assert attn(fake, 0, 0) == -1 and b"sequence_length" in native.sol_last_error()
+    rc = native.sol_pair_strides(fake, strides, None, 0, 1, 192, 2, 64, fake, fake, None)
     assert rc == -2 and b"4 .. 8192 query blocks" in native.sol_last_error()
-    rc = native.sol_pair_strides(fake, strides, None, 1, 193, 2, 64, None, fake, None)
+    rc = native.sol_pair_strides(fake, strides, None, 0, 1, 193, 2, 64, None, fake, None)
     assert rc == -1 and b"workspace" in native.sol_last_error()
+    rc = native.sol_pair_strides(fake, strides, fake, 0, 1, 193, 2, 64, fake, fake, None)
+    assert rc == -1 and b"sequence_length" in native.sol_last_error()
     bad = (ctypes.c_int64 * 3)(64 * 2 * 317, 127, 64)
-    rc = native.sol_pool_kv(fake, bad, fake, strides, None, None, 1, 317, 2, 64, fake, fake,
+    rc = native.sol_pool_kv(fake, bad, fake, strides, None, None, 0, 1, 317, 2, 64, fake, fake,
                             None, None, None, None)
     assert rc == -1 and b"aligned" in native.sol_last_error()
-    rc = native.sol_pool_kv(fake, strides, fake, strides, None, None, 1, 317, 2, 64, None, None,
+    rc = native.sol_pool_kv(fake, strides, fake, strides, None, None, 0, 1, 317, 2, 64, None, None,
                             None, None, None, None)
     assert rc == -1 and b"nothing to write" in native.sol_last_error()
+    rc = native.sol_pool_kv(fake, strides, fake, strides, fake, None, 0, 1, 317, 2, 64, fake, fake,
+                            None, None, None, None)
+    assert rc == -1 and b"sequence_length" in native.sol_last_error()
     assert native.sol_key_covariance_workspace_size(2, 3, 64) == 2 * 3 * 16 * 64 * 64 * 4
     assert native.sol_key_covariance_workspace_size(2, 3, 96) == 0
     rc = native.sol_key_covariance(fake, fake, None, 1, 317, 2, 96, fake, fake, None)

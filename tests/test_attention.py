@@ -13,7 +13,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle.sol_oracle import sol_oracle
-from sol_attn_amd import dense_attention, sol_attention
+from sol_attn_amd import _native, dense_attention, sol_attention
 from sol_testlib import HAS_GPU, assert_close, tensors
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not HAS_GPU, reason="AMD ROCm GPU required")]
@@ -35,7 +35,7 @@ GROUPS = ["1", "2"]
 @pytest.mark.parametrize("strided", [False, True])
 def test_sol_ragged_cross_attention(d, beta, strided, group, monkeypatch):
     # test_attention.py:55-69
-    monkeypatch.setenv("SOL_ATTN_GROUP", group)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", int(group))
     q, k, v = tensors(d=d, b=2, device="cuda", strided=strided)
     actual, stats = sol_attention(q, k, v, beta=beta, return_stats=True)
     ref, counts, _ = sol_oracle(q.cpu(), k.cpu(), v.cpu(), beta=beta)
@@ -86,7 +86,7 @@ def test_sol_single_token_no_empty_mass_nan():
 def test_sol_multiple_groups_and_tail(beta, group, monkeypatch):
     # test_attention.py:104-112; 17 query blocks: the last two-block
     # workgroup holds one live block.
-    monkeypatch.setenv("SOL_ATTN_GROUP", group)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", int(group))
     q, k, v = tensors(nq=1025, nk=1089, h=1, device="cuda")
     actual, stats = sol_attention(q, k, v, beta=beta, return_stats=True)
     ref, counts, _ = sol_oracle(q.cpu(), k.cpu(), v.cpu(), beta=beta)

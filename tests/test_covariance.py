@@ -68,7 +68,7 @@ def test_full_covariance_differs_from_diagonal_and_beta_zero_matches():
 
 @pytest.mark.parametrize("group", ["1", "2"])  # one- and two-block workgroups
 def test_full_covariance_ragged_windows_match_oracle(group, monkeypatch):
-    monkeypatch.setenv("SOL_ATTN_GROUP", group)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", int(group))
     x = [correlated(1, 3000, 2, 64, s)[0].cuda() for s in (9, 10, 11)]
     rows = torch.stack((torch.arange(0, 700), torch.arange(1500, 2200)))
     keys = [torch.arange(0, 1200), torch.arange(900, 3000)]

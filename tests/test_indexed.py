@@ -8,7 +8,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle.sol_oracle import sol_oracle
-from sol_attn_amd import IndexedPlan, sol_attention_indexed
+from sol_attn_amd import _native, IndexedPlan, sol_attention_indexed
 from sol_testlib import HAS_GPU
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not HAS_GPU, reason="AMD ROCm GPU required")]
@@ -76,7 +76,7 @@ def _ragged_case(seed, n=1500, heads=2, d=128):
 @pytest.mark.parametrize("group", ["1", "2"])  # one- and two-block workgroups
 @pytest.mark.parametrize("beta", [-math.inf, math.inf, 1.0, 0.0])
 def test_ragged_windows_one_call_equal_separate_calls_and_oracle(beta, group, monkeypatch):
-    monkeypatch.setenv("SOL_ATTN_GROUP", group)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", int(group))
     x, rows, keys = _ragged_case(11)
     kw = dict(protected_ranges=((0, 7),), local_tokens=64)
     p = IndexedPlan.create(rows, keys, 1500, **kw)
@@ -101,7 +101,7 @@ def test_ragged_windows_one_call_equal_separate_calls_and_oracle(beta, group, mo
 
 @pytest.mark.parametrize("group", ["1", "2"])
 def test_scatter_epilogue_equals_indexed_assignment(group, monkeypatch):
-    monkeypatch.setenv("SOL_ATTN_GROUP", group)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", int(group))
     x, rows, keys = _ragged_case(12)
     gpu = [t.cuda() for t in x]
     for plan in (IndexedPlan.create(rows, keys, 1500),
@@ -116,3 +116,39 @@ def test_scatter_epilogue_equals_indexed_assignment(group, monkeypatch):
         assert torch.equal(out, expected)
     with pytest.raises(ValueError, match="out must be"):
         sol_attention_indexed(*gpu, p, out=torch.empty_like(gpu[0]).float())
+
+
+def test_scatter_rejects_shared_rows_and_tampered_plans_stay_in_bounds():
+    x, rows, keys = _ragged_case(13)
+    gpu = [t.cuda() for t in x]
+    # Two windows with one query row in common: out= would race on it.
+    shared = torch.stack((torch.arange(64, 194), torch.arange(193, 323)))
+    p = IndexedPlan.create(shared, torch.stack([k[:80] for k in keys[:2]]), 1500).to("cuda")
+    assert p.rows_distinct is False
+    with pytest.raises(ValueError, match="share no query row"):
+        sol_attention_indexed(*gpu, p, beta=1.0, out=torch.empty_like(gpu[0]))
+    sol_attention_indexed(*gpu, p, beta=1.0)  # without out= the plan is fine
+    # A plan changed after create(): index entries outside the sequence are
+    # clamped for reads and such rows are not stored, so nothing outside
+    # Q/K/V and out is touched; the valid rows keep their results.
+    plan = IndexedPlan.create(rows, keys, 1500).to("cuda")
+    ref = sol_attention_indexed(*gpu, plan, beta=1.0)
+    rows_t = plan.rows.clone()
+    rows_t[0, 5] = -7
+    rows_t[2, 9] = 1500 + 10
+    tampered = IndexedPlan(rows_t, plan.keys, plan.protected_blocks, 1500, plan.key_lengths, True)
+    out = torch.full_like(gpu[0], 3.0)
+    sol_attention_indexed(*gpu, tampered, beta=1.0, out=out)
+    torch.cuda.synchronize()
+    # Window 1 is untouched: its rows hold exactly its result.
+    assert torch.equal(out[plan.rows[1]], ref[1])
+    # Every row the tampered plan does not name validly keeps its old value;
+    # in particular rows 0 and 1499, where the bad entries were clamped for
+    # reading, are not written.
+    valid = torch.ones_like(rows_t, dtype=torch.bool)
+    valid[0, 5] = valid[2, 9] = False
+    untouched = torch.ones(1500, dtype=torch.bool, device="cuda")
+    untouched[rows_t[valid]] = False
+    assert bool(untouched[0]) and bool(untouched[1499])
+    assert (out[untouched] == 3.0).all()
+    assert torch.isfinite(out.float()).all()

@@ -14,6 +14,7 @@ import numpy as np
 import pytest
 import torch
 
+import bench
 from oracle import sol_oracle as orc
 from sol_attn_amd import _native, dense_attention, sol_attention
 from sol_testlib import HAS_GPU, assert_close, block_smooth, tensors, to_np
@@ -121,11 +122,18 @@ def run_debug(q, k, v, beta, scale=None, local=1, kv_sink=0, q_sink=0, estimator
     return out, counts, dbg
 
 
+# In-band mismatches allowed per decision (a stated cap on top of the band).
+MAX_BAND_MISMATCH_RATE = 1e-4
+
+
 def check_routing(q, k, v, beta, scale=None, local=1, kv_sink=0, q_sink=0, query_blocks=None,
-                  max_band_mismatch=None, estimator="diagonal_covariance"):
+                  max_band_mismatch=None, estimator="diagonal_covariance", label=""):
     """Decisions vs oracle (band), outputs under identical routing, counts.
 
-    Returns ``(kernel_out, oracle_out_under_kernel_routing, qrows)``."""
+    Every mismatch must lie inside the band, and their number may not exceed
+    ``max_band_mismatch`` (default: MAX_BAND_MISMATCH_RATE of the decisions);
+    the count and the band population are printed.  Returns
+    ``(kernel_out, oracle_out_under_kernel_routing, mismatch_mask)``."""
     qn, kn, vn = to_np(q.cpu()), to_np(k.cpu()), to_np(v.cpu())
     d = qn.shape[-1]
     s = d ** -0.5 if scale is None else scale
@@ -143,17 +151,23 @@ def check_routing(q, k, v, beta, scale=None, local=1, kv_sink=0, q_sink=0, query
     qbs = np.arange(qm.shape[1]) if query_blocks is None else np.asarray(query_blocks)
     ksel_s, sel_s = ksel[:, qbs], sel[:, qbs]
     mismatch = ksel_s != sel_s
-    if mismatch.any():
-        assert math.isfinite(beta), "infinite beta routing must match exactly"
+    in_band = 0
+    if math.isfinite(beta):
         c = cut[:, qbs][..., None]
         qn_norm = np.linalg.norm(qm[:, qbs], axis=-1)[..., None]            # [B, n, H, 1]
         kn_norm = np.linalg.norm(kc, axis=-1).transpose(0, 2, 1)[:, None]   # [B, 1, H, NKB]
         band = BAND * np.maximum(np.abs(c), s * qn_norm * kn_norm)
         gap = np.abs(proxy[:, qbs] - c)
+        in_band = int((gap <= band).sum())
         outside = mismatch & (gap > band)
         assert not outside.any(), f"{int(outside.sum())} routing decisions differ outside the band"
-        if max_band_mismatch is not None:
-            assert mismatch.sum() <= max_band_mismatch
+    else:
+        assert not mismatch.any(), "infinite beta routing must match exactly"
+    cap = (max_band_mismatch if max_band_mismatch is not None
+           else int(MAX_BAND_MISMATCH_RATE * mismatch.size))
+    print(f"routing {label} beta={beta}: {mismatch.size} decisions, {int(mismatch.sum())} in-band "
+          f"mismatches (cap {cap}), {in_band} decisions inside the band", flush=True)
+    assert mismatch.sum() <= cap, f"{int(mismatch.sum())} in-band mismatches exceed the cap {cap}"
     # Kernel proxies and cutoffs agree with the oracle's to FP32 rounding.
     if math.isfinite(beta):
         kp = to_np(dbg["proxy"])[:, qbs]
@@ -170,28 +184,54 @@ def check_routing(q, k, v, beta, scale=None, local=1, kv_sink=0, q_sink=0, query
     return to_np(out.cpu())[:, rows], ref[:, rows], mismatch
 
 
+def workload(name):
+    """A bench workload's inputs (seed 0, one CPU generator, draw order Q, K, V)."""
+    cfg = bench.WORKLOADS[name]
+    q, k, v = bench.make_inputs(cfg, torch.device("cuda"))
+    return cfg, q, k, v
+
+
+@pytest.mark.parametrize("group", [1, 2])
+def test_c1_whole_call_against_oracle(group, monkeypatch):
+    # B=1, T=1024, H=8, D=64, block-smooth (noise 0.1), seed 0, beta 1, sinks
+    # 128, local 1: every query block of the call against the oracle.
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", group)
+    cfg, q, k, v = workload("selfattn-1024-smooth")
+    assert q.shape == (1, 1024, 8, 64)
+    actual, ref, _ = check_routing(q, k, v, cfg["beta"], local=cfg["local_blocks"],
+                                   kv_sink=cfg["kv_sink_tokens"], q_sink=cfg["query_sink_tokens"],
+                                   label=f"C1 form {group}")
+    assert_close(actual, ref)
+    out, stats = sol_attention(q, k, v, beta=cfg["beta"], local_blocks=cfg["local_blocks"],
+                               kv_sink_tokens=cfg["kv_sink_tokens"],
+                               query_sink_tokens=cfg["query_sink_tokens"], return_stats=True)
+    ref_all, counts, _ = orc.sol_oracle(to_np(q.cpu()), to_np(k.cpu()), to_np(v.cpu()), beta=cfg["beta"],
+                                        local_blocks=cfg["local_blocks"], kv_sink_tokens=cfg["kv_sink_tokens"],
+                                        query_sink_tokens=cfg["query_sink_tokens"])
+    assert_close(out.cpu(), ref_all)
+    np.testing.assert_array_equal(stats.exact_blocks.cpu().numpy(), counts)
+
+
 @pytest.mark.parametrize("beta", [-math.inf, 0.0, 1.0, math.inf])
 @pytest.mark.parametrize("kind", ["smooth", "random"])
 def test_c2_shape_routing_and_output(beta, kind):
-    # B=2, T=4096, H=16, D=128, sinks 128, local 1; oracle on 6 query blocks.
-    if kind == "smooth":
-        q, k, v = (block_smooth(2, 4096, 16, 128, seed=s, device="cuda") for s in (1, 2, 3))
-    else:
-        q, k, v = tensors(nq=4096, nk=4096, d=128, b=2, h=16, device="cuda", seed=0)
+    # B=2, T=4096, H=16, D=128, sinks 128, local 1, seed 0; oracle on 6 query blocks.
+    cfg, q, k, v = workload(f"selfattn-4096-{kind}")
     qbs = [0, 1, 2, 31, 32, 63]
-    actual, ref, _ = check_routing(q, k, v, beta, kv_sink=128, q_sink=128, query_blocks=qbs)
+    actual, ref, _ = check_routing(q, k, v, beta, kv_sink=cfg["kv_sink_tokens"],
+                                   q_sink=cfg["query_sink_tokens"], local=cfg["local_blocks"],
+                                   query_blocks=qbs, label=f"C2 {kind}")
     assert_close(actual, ref)
 
 
 def test_c3_ragged_cross_attention_strided_query():
-    # B=1, H=24, D=128, Tq=4096, Tk=10000, Q head-strided view, random; beta 1,
-    # kv sink 64, q sink 0, local 0.
-    g = torch.Generator(device="cuda").manual_seed(0)
-    q = torch.randn((1, 4096, 48, 128), generator=g, device="cuda", dtype=torch.bfloat16)[:, :, ::2]
-    k = torch.randn((1, 10000, 24, 128), generator=g, device="cuda", dtype=torch.bfloat16)
-    v = torch.randn((1, 10000, 24, 128), generator=g, device="cuda", dtype=torch.bfloat16)
-    actual, ref, _ = check_routing(q, k, v, 1.0, local=0, kv_sink=64, q_sink=0,
-                                   query_blocks=[0, 17, 40, 63])
+    # B=1, H=24, D=128, Tq=4096, Tk=10000, Q head-strided view, random, seed 0;
+    # beta 1, kv sink 64, q sink 0, local 0.
+    cfg, q, k, v = workload("crossattn-4096x10000-random")
+    assert q.stride(2) == 256 and k.shape[1] == 10000
+    actual, ref, _ = check_routing(q, k, v, cfg["beta"], local=cfg["local_blocks"],
+                                   kv_sink=cfg["kv_sink_tokens"], q_sink=cfg["query_sink_tokens"],
+                                   query_blocks=[0, 17, 40, 63], label="C3")
     assert_close(actual, ref)
 
 

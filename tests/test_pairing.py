@@ -77,7 +77,7 @@ def test_no_pairing_below_four_query_blocks():
 @pytest.mark.parametrize("beta", [1.0, -math.inf, 0.0])
 def test_pairing_never_changes_results(beta, d, monkeypatch):
     monkeypatch.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)  # pair these 72 query blocks
-    monkeypatch.setenv("SOL_ATTN_GROUP", "2")  # two-block workgroups (this launch is small)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", 2)  # two-block workgroups (this launch is small)
     q, k, v = (frames(8, 9, d=d, seed=s).cuda() for s in (3, 4, 5))
     ref, ref_stats = sol_attention(q, k, v, beta=beta, kv_sink_tokens=64, return_stats=True)
     monkeypatch.setattr(_native, "PAIRING", False)
@@ -97,7 +97,7 @@ def test_pairing_never_changes_results(beta, d, monkeypatch):
 
 def test_indexed_windows_pair_per_window(monkeypatch):
     monkeypatch.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)
-    monkeypatch.setenv("SOL_ATTN_GROUP", "2")  # two-block workgroups (this launch is small)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", 2)  # two-block workgroups (this launch is small)
     x = [frames(10, 6, seed=s)[0].cuda() for s in (6, 7, 8)]      # [T, H, D] NHD
     t = x[0].shape[0]
     rows = torch.stack((torch.arange(0, t // 2), torch.arange(t // 2, t)))
@@ -119,7 +119,7 @@ def test_one_and_two_block_workgroups_are_identical(shape, monkeypatch):
     q, k, v = (frames(-(-t // 576), 9, heads=h, d=d, seed=s)[:, :t].repeat(b, 1, 1, 1).cuda() for s in (12, 13, 14))
     res = {}
     for g in ("1", "2"):
-        monkeypatch.setenv("SOL_ATTN_GROUP", g)
+        monkeypatch.setattr(_native, "WORKGROUP_FORM", int(g))
         res[g] = sol_attention(q, k, v, beta=1.0, kv_sink_tokens=64, return_stats=True)
     assert torch.equal(res["1"][0], res["2"][0])
     assert torch.equal(res["1"][1].exact_blocks, res["2"][1].exact_blocks)

@@ -11,7 +11,7 @@ synchronisation in between.
 import pytest
 import torch
 
-from sol_attn_amd import dense_attention, sol_attention
+from sol_attn_amd import IndexedPlan, _native, dense_attention, sol_attention, sol_attention_indexed
 from sol_testlib import HAS_GPU, block_smooth
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not HAS_GPU, reason="AMD ROCm GPU required")]
@@ -36,24 +36,51 @@ def test_side_stream_matches_default_stream():
     assert torch.equal(dense, dense_attention(q, k, v))
 
 
-def test_graph_capture_replays_the_eager_result():
-    q, k, v = inputs()
-    eager = sol_attention(q, k, v, kv_sink_tokens=64)
+def _capture_cases():
+    """(name, setup(monkeypatch) -> call) for the three launch shapes: the
+    one-block form; the two-block form with the pairing kernels (dynamic-LDS
+    lag kernel included); indexed windows with the fused scatter into out=."""
+
+    def plain(mp):
+        q, k, v = inputs()
+        return lambda: sol_attention(q, k, v, kv_sink_tokens=64)
+
+    def paired(mp):
+        mp.setattr(_native, "WORKGROUP_FORM", 2)
+        mp.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)
+        q, k, v = inputs()
+        return lambda: sol_attention(q, k, v, kv_sink_tokens=64)
+
+    def indexed(mp):
+        q, k, v = (x[0] for x in inputs())             # NHD [2048, 4, 128]
+        rows = torch.stack((torch.arange(0, 700), torch.arange(1000, 1700)))
+        keys = [torch.arange(0, 1200), torch.arange(600, 2048)]
+        plan = IndexedPlan.create(rows, keys, 2048, protected_ranges=((0, 64),)).to("cuda")
+        out = torch.zeros_like(q)
+        return lambda: sol_attention_indexed(q, k, v, plan, beta=1.0, out=out)
+
+    return {"one-block": plain, "paired": paired, "indexed-scatter": indexed}
+
+
+@pytest.mark.parametrize("case", sorted(_capture_cases()))
+def test_graph_capture_replays_the_eager_result(case, monkeypatch):
+    call = _capture_cases()[case](monkeypatch)
+    eager = call().clone()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):  # warm-up off the default stream, as torch's capture expects
         for _ in range(2):
-            sol_attention(q, k, v, kv_sink_tokens=64)
+            call()
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        out = sol_attention(q, k, v, kv_sink_tokens=64)
+        out = call()
     for r in range(3):
         out.zero_()
         graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(out, eager), f"replay {r}"
-        again = sol_attention(q, k, v, kv_sink_tokens=64)  # eager work between replays
+        assert torch.equal(out, eager), f"{case} replay {r}"
+        again = call()  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(again, eager)
