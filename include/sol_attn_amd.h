@@ -148,10 +148,13 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
  * debug_selected (uint8) / debug_proxy (fp32): NULL or [batch, NQB, heads, NKB]
  * routing decisions and proxies (natural-log units); debug_cutoff: NULL or
  * fp32 [batch, NQB, heads].  Debug outputs are for verification, not timing.
- * workgroup_form: 0 picks the schedule by launch size; 1 or 2 forces one or
- * two query blocks per workgroup (both give bit-identical results; tests run
- * both).  No counterpart in the reference (one Triton program per query
- * block). */
+ * workgroup_form: 0 picks the schedule by launch size (1 below 512 query-block
+ * pairs, else 2); 1 or 2 force one or two query blocks per 4-wave workgroup
+ * (bit-identical results), 3 the 8-wave ping-pong workgroup (two query
+ * blocks: their common exact blocks streamed once, the rest in pairs; equal
+ * to the other forms within FP32 summation order; an experimental schedule,
+ * slower than form 2 on MI355X).  No counterpart in the reference (one
+ * Triton program per query block). */
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t sequence_length, int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,

@@ -1,0 +1,371 @@
+// Device building blocks shared by the SOL attention kernels (attention.hip,
+// attention_pp.hip): the workgroup -> query-tile maps, the FP32 online-softmax
+// state of a wave, the LDS DMA tile refill, the MFMA operand reads from the
+// swizzled tiles, and the output store.
+#pragma once
+
+#include "sol_device.h"
+#include "sol_internal.h"
+
+#define SOL_LDS __attribute__((address_space(3)))
+
+namespace sol {
+
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+
+constexpr int kXcds = 8;
+
+// Workgroup ids are dealt round-robin over the 8 XCDs.  The id -> (head, query
+// tile) map keeps every XCD on the SAME head at the same time, each on its own
+// contiguous 1/8 slice of the query tiles: neighbouring tiles share that XCD's
+// L2, and the tiles of one head (43 MB at 84,672 tokens) are the whole live
+// set of the memory-side cache.  Grid = 8 * heads * slice; ids past the end of
+// a slice return -1 (idle workgroup).
+struct TileTask {
+  int bh, tile;
+};
+
+__device__ __forceinline__ TileTask xcd_task(int i, int ntiles) {
+  const int slice = (ntiles + kXcds - 1) / kXcds;
+  const int xcd = i % kXcds, k = i / kXcds;
+  const int tile = xcd * slice + k % slice;
+  return TileTask{tile < ntiles ? k / slice : -1, tile};
+}
+
+// SOL launches dispatch the first `front` query tiles of every (entry, head)
+// ahead of the rest, head-interleaved.  With query sinks those tiles hold the
+// sink query blocks, whose workgroups stream every key block and run several
+// times longer than the others; in xcd_task order the last heads' ones would
+// start late and set the kernel's end (2 x 4,096 tokens x 16 heads with
+// 128-token sinks: 251 -> 163 us).  The remaining tiles keep the xcd_task map.
+__device__ __forceinline__ TileTask sol_task(int i, int ntiles, int front, int heads) {
+  const int nfront = front * heads;
+  if (i < nfront) return TileTask{i % heads, i / heads};
+  if (ntiles <= front) return TileTask{-1, 0};
+  TileTask t = xcd_task(i - nfront, ntiles - front);
+  t.tile += front;
+  return t;
+}
+
+__host__ __device__ inline unsigned xcd_grid(int heads, int ntiles) {
+  return unsigned(kXcds) * unsigned(heads) * unsigned((ntiles + kXcds - 1) / kXcds);
+}
+
+template <int D>
+struct Shape {
+  static constexpr int KS = D + 8;   // Q staging row stride (elements)
+  static constexpr int DC = D / 8;   // 16-byte chunks per row
+  static constexpr int KT = D / 16;  // MFMA k-steps over the head dimension
+  static constexpr int DT = D / 32;  // 32-row output tiles over the head dimension
+  static constexpr int TILE = 2 * kBlock * D;  // K + V^T tile elements per 64-wide tile
+};
+
+// One wave's FP32 online-softmax state for its 32 queries (one per lane pair).
+template <int D>
+struct State {
+  f32x16 acc[Shape<D>::DT];  // O^T: rows = features, column = this lane's query
+  float m;                   // running max, log2 units (-inf: nothing yet)
+  float den;                 // partial denominator over this lane's key rows
+};
+
+template <int D>
+__device__ __forceinline__ void state_init(State<D>& st) {
+#pragma unroll
+  for (int dt = 0; dt < Shape<D>::DT; ++dt) st.acc[dt] = zero16();
+  st.m = kNegInf;
+  st.den = 0.f;
+}
+
+// Max / sum of a value over the lane pair (l, l ^ 32) that shares one query.
+__device__ __forceinline__ float pair_max(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+
+__device__ __forceinline__ float pair_sum(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
+__device__ __forceinline__ bf16x8 pack8(const f32x16& s, int base) {
+  u32x4 pb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pb[i] = pack_bf16x2(s[base + 2 * i], s[base + 2 * i + 1]);
+  return as_bf16x8(pb);
+}
+
+// Wave-uniform copy of a 64-bit value, in an SGPR pair.  readfirstlane
+// returns a signed int: each half goes through uint32_t so that the low word
+// is zero-extended, never sign-extended into the high word.
+__device__ __forceinline__ uint64_t uniform64(uint64_t x) {
+  const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(x)));
+  const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(x >> 32)));
+  return (uint64_t(hi) << 32) | uint64_t(lo);
+}
+
+// 16-byte global -> LDS DMA per lane: lane l reads sbase + lane_bytes and its
+// bytes land at LDS address m + 16 l; sbase and m are wave-uniform.  The base
+// travels in an SGPR pair (global "saddr" form) and the per-lane part is a
+// 32-bit offset, so a refill holds no 64-bit per-lane addresses in vector
+// registers.  Issued as inline assembly so that the compiler does not drain
+// the vector memory counter before every LDS read (it cannot tell the ring's
+// buffers apart); completion is awaited explicitly with wait_vmcnt before the
+// barrier.  M0 (the LDS base register of the DMA) is saved and restored
+// around it.
+__device__ __forceinline__ void dma16(uint64_t sbase, uint32_t lane_bytes, uint32_t m) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(m), "v"(lane_bytes), "s"(sbase)
+      : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((SOL_LDS const void*)p));
+}
+
+// DMA of one K + V^T tile pair (contiguous in HBM) into an LDS buffer, in
+// kRounds rounds of one 16-byte chunk per lane: round r moves the 1 KB piece
+// of wave w at byte offset 16 (r NT + 64 w).  A refill can be issued whole,
+// or a few rounds at a time between a wave's score MFMAs, so that the wave's
+// in-order instruction stream does not stall on a burst of DMA issues.
+// Every round must be issued exactly once per refill.  Rounds are
+// unconditional (no branch splits the MFMA schedule): a stream with no
+// further tile refills the slot with a tile it already read, into a slot no
+// later tile uses.
+template <int D, int NT>
+struct TileRefill {
+  static constexpr int kChunks = Shape<D>::TILE / 8;  // 16-byte chunks per tile pair
+  static constexpr int kRounds = kChunks / NT;
+  static_assert(kChunks % NT == 0, "tile pair must split evenly over the workgroup");
+  uint64_t src;         // wave-uniform address of this wave's first chunk
+  uint32_t lds;         // wave-uniform LDS address of the same chunk
+  uint32_t lane_bytes;  // 16 * lane
+
+  __device__ __forceinline__ TileRefill(const uint16_t* tile, uint32_t dst_lds, int wave, int lane)
+      : src(uniform64(reinterpret_cast<uint64_t>(tile) + uint64_t(wave) * (kWave * 16))),
+        lds(uint32_t(__builtin_amdgcn_readfirstlane(dst_lds + uint32_t(wave) * (kWave * 16)))),
+        lane_bytes(uint32_t(lane) * 16u) {}
+
+  __device__ __forceinline__ void round(int r) const {
+    // The round's offset passes through an empty asm so that it is formed
+    // here from an immediate, not kept live in registers of its own across
+    // the whole stream.
+    uint32_t off = uint32_t(r) * (NT * 16);
+    asm volatile("" : "+s"(off));
+    dma16(src + off, lane_bytes, lds + off);
+  }
+  __device__ __forceinline__ void all() const {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) round(r);
+  }
+  // The rounds that belong after step k of an N-step schedule.
+  template <int N>
+  __device__ __forceinline__ void after_step(int k) const {
+#pragma unroll
+    for (int r = k * kRounds / N; r < (k + 1) * kRounds / N; ++r) round(r);
+  }
+};
+
+// A refill with nothing to load (single-slot ring).
+struct NoRefill {
+  __device__ __forceinline__ void all() const {}
+  template <int N>
+  __device__ __forceinline__ void after_step(int) const {}
+};
+
+template <int D, int NT>
+__device__ __forceinline__ void tile_dma(const uint16_t* src, uint32_t dst_lds, int wave, int lane) {
+  TileRefill<D, NT>(src, dst_lds, wave, lane).all();
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier without a memory fence: LDS DMA completion is awaited
+// explicitly with s_waitcnt vmcnt, so the in-flight prefetch of the next tile
+// is not drained here.  The "memory" clobber keeps LDS accesses on their side.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Returns x through an empty asm statement.  Applied to a lane index inside a
+// tile loop, it makes the addresses derived from it be formed per tile rather
+// than hoisted out of the loop, where dozens of lane-dependent offsets would
+// stay live (and spill) for the whole stream.
+__device__ __forceinline__ int fresh(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// Key row (inside a 64-row tile) of element e of this lane's 32-key half t:
+// in the 32x32 MFMA result layout, lane half hh holds rows
+// 8 (e / 4) + 4 hh + e % 4 of each 32-row half.
+__device__ __forceinline__ int tile_row(int t, int e, int hh) {
+  return 32 * t + 8 * (e >> 2) + 4 * hh + (e & 3);
+}
+
+// Materialises a value at this point of the instruction stream, so that the
+// work producing it stays ahead of a following branch (where the scheduler
+// can overlap it with matrix-core work) instead of being sunk past it.
+template <typename T>
+__device__ __forceinline__ void pin(T& x) {
+  asm volatile("" : "+v"(x));
+}
+
+// acc *= alpha, in place (the accumulator keeps its registers on both sides
+// of the rare rescale branch instead of being copied).
+template <int D>
+__device__ __forceinline__ void rescale_acc(State<D>& st, float alpha) {
+#pragma unroll
+  for (int dt = 0; dt < Shape<D>::DT; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(st.acc[dt][e]) : "v"(alpha));
+}
+
+// Lazy online softmax: the running max m (log2 units, per query) moves only
+// when some query's max exceeds it by more than kRescaleSlack.  Otherwise the
+// probabilities exp2(s c - m) may exceed 1 by up to 2^kRescaleSlack, which
+// FP32 sums and BF16 products carry at unchanged relative precision; acc and
+// den always share m, so O = acc / den is unaffected.  The common case has
+// no data-dependent branch, so a half's softmax can be spread between
+// matrix-core instructions.
+constexpr float kRescaleSlack = 8.f;
+
+// Softmax of one 32-key half of raw scores s (absent keys -inf; c = scale *
+// log2(e)), in 8 stages that a caller places between MFMAs: max; the
+// wave-uniform rescale decision, new max and alpha; 4 x 4 probabilities
+// exp2(s c - m); BF16 packing; den update.  The caller multiplies acc by
+// alpha when `rescale` is set.
+template <int D>
+struct HalfSoftmax {
+  f32x16 s;
+  float mx, alpha, neg_m, lsum;
+  bool rescale;
+  bf16x8 pw[2];  // packed BF16 probabilities, keys 0..15 / 16..31 of the half
+
+  __device__ __forceinline__ void stage(int k, State<D>& st, float c) {
+    if (k == 0) {
+      mx = kNegInf;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[e]);
+    } else if (k == 1) {
+      mx = pair_max(mx) * c;
+      rescale = __builtin_amdgcn_ballot_w64(mx > st.m + kRescaleSlack) != 0;
+      const float mnew = rescale ? fmaxf(st.m, mx) : st.m;
+      alpha = fast_exp2(st.m - (mnew == kNegInf ? 0.f : mnew));  // 1 without a rescale (0 before any key)
+      st.m = mnew;
+      neg_m = mnew == kNegInf ? 0.f : -mnew;
+      lsum = 0.f;
+    } else if (k < 6) {
+#pragma unroll
+      for (int e = 4 * (k - 2); e < 4 * (k - 1); ++e) {
+        const float pe = fast_exp2(fmaf(s[e], c, neg_m));
+        s[e] = pe;
+        lsum += pe;
+      }
+    } else if (k == 6) {
+      pw[0] = pack8(s, 0);
+      pw[1] = pack8(s, 8);
+      pin(pw[0]);
+      pin(pw[1]);
+    } else {
+      st.den = st.den * alpha + lsum;
+      pin(st.den);
+    }
+  }
+  // The B operand of the P V product for keys 16 c4 .. 16 c4 + 15 of the half.
+  __device__ __forceinline__ bf16x8 pb(int c4) const { return pw[c4]; }
+  // Part k of n (n = 4 or 8) of the stages.
+  template <int N>
+  __device__ __forceinline__ void part(int k, State<D>& st, float c) {
+#pragma unroll
+    for (int i = k * 8 / N; i < (k + 1) * 8 / N; ++i) stage(i, st, c);
+  }
+};
+
+// This lane's element offsets of its MFMA operand reads inside a K + V^T
+// tile pair (see TileLayout): K fragment (t, ks) at k_row + 32 t D +
+// (k_x ^ 16 ks), V^T fragment (t, c4, dt) at kElems + v_row + 2048 dt +
+// (v_x ^ (32 t + 16 c4)); the per-read parts are immediates or one XOR-add.
+template <int D>
+struct FragLane {
+  int k_row, k_x, v_row, v_x;
+  __device__ __forceinline__ FragLane(int col, int hh)
+      : k_row(col * D),
+        k_x(TileLayout<D>::k_lane_xor(col, hh)),
+        v_row(TileLayout<D>::kElems + col * kBlock),
+        v_x(TileLayout<D>::vt_lane_xor(col, hh)) {}
+  __device__ __forceinline__ u32x4 k(const uint16_t* buf, int t, int ks) const {
+    return *reinterpret_cast<const u32x4*>(buf + k_row + 32 * t * D + (k_x ^ (16 * ks)));
+  }
+  __device__ __forceinline__ u32x4 v(const uint16_t* buf, int t, int c4, int dt) const {
+    return *reinterpret_cast<const u32x4*>(buf + v_row + 32 * kBlock * dt + (v_x ^ (32 * t + 16 * c4)));
+  }
+};
+
+// Ends a scheduling chunk: nothing moves across it, so the hand-placed
+// interleave of matrix-core, LDS, DMA and VALU work below is kept.
+__device__ __forceinline__ void chunk_end() { __builtin_amdgcn_sched_barrier(0); }
+
+template <int D>
+__device__ __forceinline__ void store_output(const AttnParams& p, int b, int h, int t, int hh,
+                                             const State<D>& st) {
+  using S = Shape<D>;
+  const float den = pair_sum(st.den);
+  if (t >= p.Tq) return;
+  int64_t row = int64_t(b) * p.Tq + t;
+  if (p.out_index) {
+    row = p.out_index[row];
+    if (row < 0 || row >= p.out_rows) return;  // outside the output: not stored
+  }
+  uint16_t* orow = p.out + (row * p.H + h) * D;
+#pragma unroll
+  for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      u32x2 o;
+      o[0] = pack_bf16x2(__fdiv_rn(st.acc[dt][4 * k4], den), __fdiv_rn(st.acc[dt][4 * k4 + 1], den));
+      o[1] = pack_bf16x2(__fdiv_rn(st.acc[dt][4 * k4 + 2], den), __fdiv_rn(st.acc[dt][4 * k4 + 3], den));
+      *reinterpret_cast<u32x2*>(orow + dt * 32 + 8 * k4 + 4 * hh) = o;
+    }
+}
+
+// Barrier that publishes this workgroup's LDS accesses (no global-memory
+// fence, so the ring's DMA in flight is not drained).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Approximated blocks of centroid tile ct for one query block: valid blocks
+// whose routing bit is clear.
+__device__ __forceinline__ uint64_t tile_approx(const uint32_t* mask, int ct, int nkb) {
+  const int nvalid = min(64, nkb - 64 * ct);
+  const uint64_t valid = nvalid == 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+  const uint64_t sel = uint64_t(mask[2 * ct]) | (uint64_t(mask[2 * ct + 1]) << 32);
+  return valid & ~sel;
+}
+
+
+// Query block of slot s (= group index * G + member) when group members are
+// query blocks `stride` apart: within each run of 2 * stride blocks, block i
+// pairs with block i + stride; blocks past the last full run keep their slot.
+// A bijection on [0, n); slots >= n stay >= n (no query block).
+__device__ __forceinline__ int slot_block(int s, int n, int stride) {
+  if (stride <= 0) return s;
+  const int run = 2 * stride;
+  if (s >= (n / run) * run) return s;
+  const int w = s % run;
+  return (s / run) * run + (w >> 1) + (w & 1) * stride;
+}
+
+}  // namespace
+
+}  // namespace sol

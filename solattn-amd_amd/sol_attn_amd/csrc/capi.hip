@@ -239,8 +239,8 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: Q needs 16-byte aligned rows and positive strides");
   if ((query_index || out_index) && sequence_length <= 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_index / out_index need sequence_length > 0");
-  if (workgroup_form < 0 || workgroup_form > 2)
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: workgroup_form must be 0, 1 or 2");
+  if (workgroup_form < 0 || workgroup_form > 3)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: workgroup_form must be 0, 1, 2 or 3");
   if (!std::isfinite(scale) || scale <= 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: scale must be finite and positive");
   if (std::isnan(beta)) return fail(SOL_ERR_INVALID, "sol_attention_fwd: beta must not be NaN");

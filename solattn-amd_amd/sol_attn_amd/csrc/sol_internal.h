@@ -75,7 +75,8 @@ struct AttnParams {
   int force;          // 0 finite beta, 1 beta = -inf (all exact), 2 beta = +inf
   int local_blocks;   // < 0 disables the local band
   int kv_sink_blocks, q_sink_blocks;
-  int workgroup_form;  // 0: by launch size; 1 / 2: query blocks per SOL workgroup
+  int workgroup_form;  // 0: by launch size; 1 / 2: query blocks per workgroup of
+                       // sol_attention_kernel; 3: the ping-pong kernel (two blocks)
 };
 
 // Indexed-window protection (plan.hip).
@@ -91,6 +92,8 @@ struct PlanParams {
 
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream);
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream);
+hipError_t launch_sol_pp(const AttnParams& p, int D, hipStream_t stream);
+hipError_t launch_dense_pp(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_dense(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream);
 hipError_t launch_plan_protection(const PlanParams& p, hipStream_t stream);

@@ -173,7 +173,7 @@ def test_c_abi_rejects_bad_arguments_without_launching():
                                   None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None,
                                   None, None, None, 0, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
-    assert attn(None, 0, 3) == -1 and b"workgroup_form" in native.sol_last_error()
+    assert attn(None, 0, 4) == -1 and b"workgroup_form" in native.sol_last_error()
     assert attn(fake, 0, 0) == -1 and b"sequence_length" in native.sol_last_error()
     rc = native.sol_pair_strides(fake, strides, None, 0, 1, 192, 2, 64, fake, fake, None)
     assert rc == -2 and b"4 .. 8192 query blocks" in native.sol_last_error()

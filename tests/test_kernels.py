@@ -191,7 +191,7 @@ def workload(name):
     return cfg, q, k, v
 
 
-@pytest.mark.parametrize("group", [1, 2])
+@pytest.mark.parametrize("group", [1, 2, 3])
 def test_c1_whole_call_against_oracle(group, monkeypatch):
     # B=1, T=1024, H=8, D=64, block-smooth (noise 0.1), seed 0, beta 1, sinks
     # 128, local 1: every query block of the call against the oracle.
