@@ -45,6 +45,8 @@ extern "C" {
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
 
+#define SOL_NOALLOC_SCRATCH_BYTES (128ll << 20) /* device workspace of sol_attention_noalloc */
+
 #define SOL_OK 0
 #define SOL_ERR_INVALID (-1)
 #define SOL_ERR_UNSUPPORTED (-2)
@@ -194,6 +196,30 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides,
                   int64_t batch, int64_t query_tokens, int64_t key_tokens,
                   int64_t heads, int64_t head_dim, double scale,
                   void* tiles, void* out, void* stream);
+
+/* All-in SOL attention that allocates nothing: sol_pool_kv followed by
+ * sol_attention_fwd (BTHD inputs; no index, plan protection, covariance or
+ * debug outputs), with the pooled key buffers in a library-owned device array
+ * of SOL_NOALLOC_SCRATCH_BYTES per GPU instead of caller workspace.  Same
+ * results as those two calls (bit-identical).  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  The caller passes Q/K/V, out (contiguous BF16 [batch,
+ * query_tokens, heads, head_dim]) and counts (NULL or int32 [batch, NQB,
+ * heads]); arguments as in sol_attention_fwd.  The pooled keys take about
+ * 2 * head_dim * 2 bytes per key token and head (the K / V^T tiles) plus the
+ * centroids: problems needing more than SOL_NOALLOC_SCRATCH_BYTES (128 MiB:
+ * batch * heads * key_tokens up to about 250,000 at head_dim 128, 500,000 at
+ * 64) return SOL_ERR_UNSUPPORTED before any GPU work.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (different streams or threads) race and must be
+ * serialised by the caller. */
+int sol_attention_noalloc(const void* q, const int64_t* q_strides,
+                          const void* k, const int64_t* k_strides,
+                          const void* v, const int64_t* v_strides,
+                          int64_t batch, int64_t query_tokens, int64_t key_tokens,
+                          int64_t heads, int64_t head_dim, double scale, double beta,
+                          int64_t local_blocks, int64_t kv_sink_tokens,
+                          int64_t query_sink_tokens, void* out, int32_t* counts, void* stream);
 
 #ifdef __cplusplus
 }

@@ -45,6 +45,8 @@ _SIGNATURES = {
     "sol_plan_protection": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
     "sol_key_covariance_workspace_size": ([_i64, _i64, _i64], ctypes.c_int64),
     "sol_key_covariance": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "sol_attention_noalloc": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
+                               _dbl, _dbl, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
 }
 
 

@@ -2,6 +2,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "sol_attn_amd.h"
@@ -54,6 +55,36 @@ sol::TokenRows rows_of(const void* base, const int64_t* strides, const int64_t* 
   r.T = int(tokens);
   return r;
 }
+
+// Workspace of sol_attention_noalloc: the pooled key buffers live in this
+// file-scope device array instead of caller or library allocations.  Each GPU
+// holds its own copy until the process ends.  Host code never passes the
+// array's name to a kernel: it passes the per-device address that
+// hipGetSymbolAddress returns (scratch_on_current_device).
+__device__ __align__(256) uint8_t scratch[SOL_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device.
+int scratch_on_current_device(void** ptr) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return hip_status(err);
+  if (dev < 0 || dev >= kMaxDevices) return fail(SOL_ERR_UNSUPPORTED, "sol_attention_noalloc: device index too large");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return hip_status(err);
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return SOL_OK;
+}
+
+int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
 }  // namespace
 
@@ -326,6 +357,43 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
   p.scale = float(scale);
   p.scale_log2 = float(scale * 1.4426950408889634);
   return hip_status(sol::launch_dense(p, int(head_dim), static_cast<hipStream_t>(stream)));
+}
+
+int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k,
+                          const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                          int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                          int64_t head_dim, double scale, double beta, int64_t local_blocks,
+                          int64_t kv_sink_tokens, int64_t query_sink_tokens, void* out,
+                          int32_t* counts, void* stream) {
+  if (!shape_ok(batch, query_tokens, heads, head_dim) || !shape_ok(batch, key_tokens, heads, head_dim))
+    return fail(SOL_ERR_INVALID, "sol_attention_noalloc: unsupported shape (head_dim must be 64 or 128)");
+  // The sol_pool_kv buffers, 256-byte aligned, in the order sol_pool_sizes lists them.
+  int64_t sizes[4];
+  if (sol_pool_sizes(batch, key_tokens, heads, head_dim, sizes) != SOL_OK) return SOL_ERR_INVALID;
+  const bool moments = std::isfinite(beta);
+  const int64_t off_tiles = align256(sizes[0]);
+  const int64_t off_sums = off_tiles + align256(sizes[1]);
+  const int64_t off_mean = off_sums + align256(sizes[2]);
+  const int64_t off_var = off_mean + align256(sizes[3]);
+  const int64_t need = moments ? off_var + align256(sizes[3]) : off_sums;
+  if (need > SOL_NOALLOC_SCRATCH_BYTES)
+    return fail(SOL_ERR_UNSUPPORTED,
+                "sol_attention_noalloc: the pooled keys need more than SOL_NOALLOC_SCRATCH_BYTES "
+                "(128 MiB); use sol_pool_kv + sol_attention_fwd with caller workspace");
+  void* base = nullptr;
+  const int rc = scratch_on_current_device(&base);
+  if (rc != SOL_OK) return rc;
+  uint8_t* ws = static_cast<uint8_t*>(base);
+  float* sums = moments ? reinterpret_cast<float*>(ws + off_sums) : nullptr;
+  float* mean = moments ? reinterpret_cast<float*>(ws + off_mean) : nullptr;
+  float* var = moments ? reinterpret_cast<float*>(ws + off_var) : nullptr;
+  const int prc = pool_checked("sol_attention_noalloc", k, k_strides, v, v_strides, nullptr, nullptr, 0, batch,
+                               key_tokens, heads, head_dim, ws, ws + off_tiles, sums, mean, var, stream);
+  if (prc != SOL_OK) return prc;
+  return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
+                           head_dim, ws + off_tiles, ws, mean, var, nullptr, nullptr, nullptr, scale, beta,
+                           local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr, counts, nullptr,
+                           nullptr, nullptr, 0, stream);
 }
 
 }  // extern "C"

@@ -207,6 +207,21 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     assert rc == -1 and b"required" in native.sol_last_error()
 
 
+def test_noalloc_rejects_problems_beyond_its_workspace_without_launching():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("libsol_attn_amd.so not built")
+    native = _native.library()
+    strides = (ctypes.c_int64 * 3)(16 * 128 * 20000, 16 * 128, 128)
+    fake = ctypes.c_void_p(1 << 20)   # never dereferenced: the size check fails first
+    # 1 x 20,000 keys x 16 heads at D = 128 needs about 160 MiB of pooled keys.
+    rc = native.sol_attention_noalloc(fake, strides, fake, strides, fake, strides, 1, 20000, 20000, 16, 128,
+                                      0.088, 1.0, 1, 0, 0, fake, None, None)
+    assert rc == -2 and b"SOL_NOALLOC_SCRATCH_BYTES" in native.sol_last_error()
+    rc = native.sol_attention_noalloc(fake, strides, fake, strides, fake, strides, 1, 200, 200, 16, 96,
+                                      0.088, 1.0, 1, 0, 0, fake, None, None)
+    assert rc == -1 and b"head_dim" in native.sol_last_error()
+
+
 def test_ragged_plan_matches_oracle_per_window():
     from oracle.sol_oracle import plan_protection
     rng = np.random.default_rng(21)
