@@ -337,6 +337,62 @@ def threshold_experiment(q, k, v, kw, diag_out, diag_density):
                 "full_covariance": {"ms": full_ms, "density": full_stats.density(), **err(full_out)}}
 
 
+def qk_int8_experiment(q, k, v, kw, cfg, bf16_out, bf16_counts, oracle_blocks):
+    """The INT8-QK variant (the reference roadmap's quantised-QK experiment)
+    against its BF16 control: the all-in call and the attention kernel alone,
+    each timed with HIP events; routing (which stays BF16) compared; the
+    output error against the BF16 kernel, the dense BF16 control and, on
+    `oracle_blocks` sampled query blocks, against both oracles."""
+    from oracle import sol_oracle as orc
+    from sol_attn_amd import _native, dense_attention, sol_attention
+    d = q.shape[-1]
+    scale = d ** -0.5
+    args = (scale, kw["beta"], cfg["local_blocks"], cfg["kv_sink_tokens"], cfg["query_sink_tokens"])
+    with torch.no_grad():
+        out8, stats8 = sol_attention(q, k, v, return_stats=True, qk_precision="int8", **kw)
+        ms = {prec: event_ms(lambda: sol_attention(q, k, v, qk_precision=prec, **kw), 5)
+              for prec in ("bf16", "int8")}
+        attn_ms = {}
+        for prec in ("bf16", "int8"):
+            pooled = _native.pool_kv(k, v, moments=True, qk_int8=prec == "int8")
+            attn_ms[prec] = event_ms(lambda: _native.attend(q, pooled, *args), 5)
+            del pooled
+        every_block = dict(kw, beta=-math.inf)
+        all_exact_ms = {prec: event_ms(lambda: sol_attention(q, k, v, qk_precision=prec, **every_block), 3)
+                        for prec in ("bf16", "int8")}
+        quant_ms = event_ms(lambda: _native.pool_kv(k, v, moments=True, qk_int8=True), 5) - \
+            event_ms(lambda: _native.pool_kv(k, v, moments=True), 5)
+        control = dense_attention(q, k, v).float()
+
+    def err(x, ref):
+        delta = x.float() - ref.float()
+        return {"rel_l2": (delta.norm() / ref.float().norm()).item(), "max_abs": delta.abs().max().item()}
+
+    qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
+    okw = dict(beta=kw["beta"], scale=scale, local_blocks=cfg["local_blocks"],
+               kv_sink_tokens=cfg["kv_sink_tokens"], query_sink_tokens=cfg["query_sink_tokens"],
+               query_blocks=oracle_blocks)
+    rows = np.concatenate([np.arange(64 * x, min(q.shape[1], 64 * x + 64)) for x in oracle_blocks])
+    ref8, _, _ = orc.sol_oracle(qn, kn, vn, qk_precision="int8", **okw)
+    ref16, _, _ = orc.sol_oracle(qn, kn, vn, **okw)
+    got8 = torch.from_numpy(out8[:, rows].float().cpu().numpy())
+    got16 = torch.from_numpy(bf16_out[:, rows].float().cpu().numpy())
+    ref8, ref16 = torch.from_numpy(ref8[:, rows]), torch.from_numpy(ref16[:, rows])
+    return {"variant": "INT8 QK on the exact blocks (Q per row, K per 64-key block, symmetric, "
+                       "v_mfma_i32_32x32x32_i8); routing, centroid terms and P V stay BF16",
+            "control": "the same call with BF16 QK",
+            "ms_per_call": ms, "attention_kernel_ms": attn_ms, "speedup_attention_kernel":
+                attn_ms["bf16"] / attn_ms["int8"],
+            "key_quantisation_ms": quant_ms,
+            "ms_per_call_every_block_exact": all_exact_ms,
+            "routing_identical": bool(torch.equal(stats8.exact_blocks, bf16_counts)),
+            "int8_vs_bf16_kernel": err(out8, bf16_out),
+            "int8_vs_dense_control": err(out8, control), "bf16_vs_dense_control": err(bf16_out, control),
+            "oracle_sample_query_blocks": list(map(int, oracle_blocks)),
+            "int8_kernel_vs_int8_oracle": err(got8, ref8), "int8_kernel_vs_bf16_oracle": err(got8, ref16),
+            "bf16_kernel_vs_bf16_oracle": err(got16, ref16)}
+
+
 def pool_bytes(b, tk, h, d, nkb, moments):
     """Algorithmic bytes of the pooling pass (read K and V once; write the K / V
     block centroids and, with moments, read them back for the mean and
@@ -436,6 +492,12 @@ def measure(name, cfg, beta, args, dev, headline):
     }
     if headline and finite and not args.no_threshold_experiment:
         result["threshold_experiment"] = threshold_experiment(q, k, v, kw, out, density)
+    if finite and not args.no_qk_int8 and (headline or (name.startswith("selfattn-4096") and beta == 1.0)):
+        with torch.no_grad():
+            _, bf16_counts = _native.launch_sol(q, k, v, scale, beta, cfg["local_blocks"], cfg["kv_sink_tokens"],
+                                                cfg["query_sink_tokens"], True)
+        result["qk_int8_experiment"] = qk_int8_experiment(
+            q, k, v, kw, cfg, out, bf16_counts, sample_blocks(-(-tq // 64), 2 if headline else 4))
     if headline and "frames" in cfg and not args.no_windows:
         result["indexed_windows"] = bench_windows(q, k, v, cfg, max(3, args.steps // 2), not args.no_cpu)
     if not args.no_cpu:
@@ -470,6 +532,8 @@ def main():
                     help="skip the indexed frame-window measurement on the same field")
     ap.add_argument("--no-threshold-experiment", action="store_true",
                     help="skip the full- vs diagonal-covariance threshold comparison")
+    ap.add_argument("--no-qk-int8", action="store_true",
+                    help="skip the INT8-QK experiment (run at beta=1 on the headline and 4,096-token workloads)")
     ap.add_argument("--copy-gib", type=float, default=0.0,
                     help="also run a device copy of this many GiB (HBM counter calibration)")
     args = ap.parse_args()

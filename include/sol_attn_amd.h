@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 6
+#define SOL_ABI_VERSION 7
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
 
@@ -150,6 +150,12 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
  * debug_selected (uint8) / debug_proxy (fp32): NULL or [batch, NQB, heads, NKB]
  * routing decisions and proxies (natural-log units); debug_cutoff: NULL or
  * fp32 [batch, NQB, heads].  Debug outputs are for verification, not timing.
+ * qk_int8_tiles / qk_int8_scales: NULL (BF16 scores, the reference's
+ * arithmetic) or the output of sol_quantize_keys: the quantised-QK
+ * experiment of the reference's roadmap (ROADMAP.md:14-16; not implemented by
+ * the reference), where exact blocks take S = s_q s_k (Q8 . K8) on the INT8
+ * matrix cores, Q8 = the query row at one scale s_q = max|q| / 127; routing,
+ * centroid terms and P V stay BF16 (forms 0-2 only).
  * workgroup_form: 0 picks the schedule by launch size (1 below 512 query-block
  * pairs, else 2); 1 or 2 force one or two query blocks per 4-wave workgroup
  * (bit-identical results), 3 the 8-wave ping-pong workgroup (two query
@@ -167,7 +173,18 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
+                      const void* qk_int8_tiles, const float* qk_int8_scales,
                       int workgroup_form, void* stream);
+
+/* INT8 K tiles for the quantised-QK experiment of sol_attention_fwd: per key
+ * block of the tile pairs that sol_pool_kv wrote (tiles, as in
+ * sol_pool_sizes), one scale s_k = max|K| / 127 over the block (k8_scales,
+ * fp32 [batch, heads, NKB]) and K8 = rint(K * 127 / max|K|) clamped to +-127
+ * (k8_tiles, int8 [batch, heads, NKB, 64 * head_dim]; 16-byte chunk c of row r
+ * at chunk c ^ ((r >> 1) & 7) for head_dim 128, c ^ ((r >> 2) & 3) for 64).
+ * No counterpart in the reference (ROADMAP.md:14-16 asks for the experiment). */
+int sol_quantize_keys(const void* tiles, int64_t batch, int64_t key_tokens, int64_t heads,
+                      int64_t head_dim, void* k8_tiles, float* k8_scales, void* stream);
 
 /* Packed-block protection of indexed windows, built on the GPU: the
  * protection part of `IndexedPlan.create` (indexed.py:27-62).  Block (w, qb,

@@ -198,6 +198,37 @@ THRESHOLD_ESTIMATORS = ("diagonal_covariance", "full_covariance")
 
 
 # ----------------------------------------------------------------------------
+# INT8 QK (the quantised-score experiment of the reference's roadmap,
+# ROADMAP.md:14-16; the reference does not implement it)
+# ----------------------------------------------------------------------------
+
+def quantize_sym(x: np.ndarray, axes) -> tuple:
+    """Symmetric INT8 quantisation over ``axes``: ``amax = max|x|``,
+    ``q = clip(rint(x * float32(127 / amax)), -127, 127)`` (round half to
+    even), ``scale = amax / 127`` (float32 arithmetic; an all-zero group gets
+    scale 0 and zeros).  Returns ``(q as float32 integers, scale)`` with the
+    scale keeping ``axes`` as size-1 dimensions."""
+    x = np.asarray(x, dtype=np.float32)
+    amax = np.abs(x).max(axis=axes, keepdims=True)
+    with np.errstate(divide="ignore"):
+        inv = np.where(amax > 0, np.float32(127.0) / amax, np.float32(0.0)).astype(np.float32)
+    q = np.clip(np.rint((x * inv).astype(np.float32)), -127, 127).astype(np.float32)
+    return q, (amax / np.float32(127.0)).astype(np.float32)
+
+
+def quantize_keys(k: np.ndarray) -> tuple:
+    """Per 64-key block and head one scale: ``k`` ``[B, Tk, H, D]`` ->
+    ``(k8 [B, Tk, H, D], scale [B, NKB, H])`` (the tail block's absent rows
+    count as zeros)."""
+    b, tk, h, d = k.shape
+    nkb = -(-tk // BLOCK)
+    pad = np.zeros((b, nkb * BLOCK, h, d), np.float32)
+    pad[:, :tk] = k
+    q, sc = quantize_sym(pad.reshape(b, nkb, BLOCK, h, d), axes=(2, 4))
+    return q.reshape(b, nkb * BLOCK, h, d)[:, :tk], sc.reshape(b, nkb, h)
+
+
+# ----------------------------------------------------------------------------
 # Routing
 # ----------------------------------------------------------------------------
 
@@ -261,19 +292,24 @@ def route(q: np.ndarray, kc: np.ndarray, cut: np.ndarray, *, beta: float, scale:
 # Attention
 # ----------------------------------------------------------------------------
 
-def _attend(qrows, k, v, kc, vc, sel_rows, lengths, scale, dtype):
+def _attend(qrows, k, v, kc, vc, sel_rows, lengths, scale, dtype, exact_scores=None):
     """One masked softmax over exact tokens and centroid virtual tokens.
 
     ``qrows``: ``[R, D]``; ``sel_rows``: ``[R, NKB]`` routing of each row's
     query block.  Selected blocks contribute every valid token
-    (``reference.py:244-246``); the rest contribute ``Kc_j`` with logit
-    ``+ ln(len_j)`` and value ``Vc_j`` (``reference.py:247-250``).
+    (``reference.py:54-57``); the rest contribute ``Kc_j`` with logit
+    ``+ ln(len_j)`` and value ``Vc_j`` (``reference.py:58-61``).
+    ``exact_scores`` (``[R, Tk]``, natural-log units) replaces ``Q K^T * scale``
+    for the exact tokens (the INT8-QK experiment).
     """
     tk = k.shape[0]
     nkb = kc.shape[0]
     token_block = np.arange(tk) // BLOCK
     qrows = qrows.astype(dtype)
-    s_exact = (qrows @ k.astype(dtype).T) * dtype(scale)                      # [R, Tk]
+    if exact_scores is None:
+        s_exact = (qrows @ k.astype(dtype).T) * dtype(scale)                  # [R, Tk]
+    else:
+        s_exact = exact_scores.astype(dtype)
     s_cent = (qrows @ kc.astype(dtype).T) * dtype(scale) + np.log(lengths.astype(dtype))  # [R, NKB]
     m_exact = sel_rows[:, token_block]
     m_cent = ~sel_rows
@@ -292,7 +328,7 @@ def sol_oracle(q, k, v, *, beta: float = 1.0, scale: Optional[float] = None,
                local_blocks: int = 1, kv_sink_tokens: int = 0, query_sink_tokens: int = 0,
                protected_blocks=None, query_blocks: Optional[Iterable[int]] = None,
                selected: Optional[np.ndarray] = None, dtype=np.float32,
-               threshold_estimator: str = "diagonal_covariance"):
+               threshold_estimator: str = "diagonal_covariance", qk_precision: str = "bf16"):
     """FP32 SOL oracle, ``reference.py:18-66`` restated.
 
     ``q``: ``[B, Tq, H, D]``; ``k``/``v``: ``[B, Tk, H, D]``; BF16 values held
@@ -305,6 +341,9 @@ def sol_oracle(q, k, v, *, beta: float = 1.0, scale: Optional[float] = None,
     definition in double precision (brute-force check).
     ``threshold_estimator="full_covariance"`` replaces the diagonal variance
     of the cutoff with the full key covariance (``cutoffs_full``).
+    ``qk_precision="int8"`` scores the exact tokens as ``s_q s_k (Q8 . K8)``
+    (``quantize_sym`` per query row, ``quantize_keys`` per key block); routing,
+    centroid terms and values are unchanged.
 
     Returns ``out`` (float32, NaN outside ``query_blocks``), ``counts``
     (int32 ``[B, NQB, H]``, -1 outside ``query_blocks``) and an ``info`` dict
@@ -335,6 +374,12 @@ def sol_oracle(q, k, v, *, beta: float = 1.0, scale: Optional[float] = None,
     if selected is not None:
         sel = _as_bool(selected).copy()
     lengths = np.minimum(BLOCK, tk - BLOCK * np.arange(nkb)).astype(np.float32)
+    if qk_precision not in ("bf16", "int8"):
+        raise ValueError("qk_precision must be 'bf16' or 'int8'")
+    if qk_precision == "int8":
+        q8, sq = quantize_sym(q, axes=3)                  # [B, Tq, H, D], [B, Tq, H, 1]
+        k8, sk = quantize_keys(k)                         # [B, Tk, H, D], [B, NKB, H]
+        sk_tok = np.repeat(sk, BLOCK, axis=1)[:, :tk]     # [B, Tk, H]
     blocks = list(range(nqb)) if query_blocks is None else [int(x) for x in query_blocks]
     out = np.full(q.shape, np.nan, np.float32)
     counts = np.full((b, nqb, h), -1, np.int32)
@@ -344,8 +389,13 @@ def sol_oracle(q, k, v, *, beta: float = 1.0, scale: Optional[float] = None,
                 rows = np.concatenate([np.arange(qb * BLOCK, min(tq, (qb + 1) * BLOCK))
                                        for qb in chunk])
                 sel_rows = sel[bi, rows // BLOCK, hi]
+                exact = None
+                if qk_precision == "int8":
+                    ints = q8[bi, rows, hi] @ k8[bi, :, hi].T           # exact integers in float32
+                    exact = (ints.astype(np.float64) * sq[bi, rows, hi] * sk_tok[bi, :, hi][None, :]
+                             * scale)
                 res = _attend(q[bi, rows, hi], k[bi, :, hi], v[bi, :, hi], kc[bi, :, hi],
-                              vc[bi, :, hi], sel_rows, lengths, scale, dtype)
+                              vc[bi, :, hi], sel_rows, lengths, scale, dtype, exact)
                 out[bi, rows, hi] = res.astype(np.float32)
                 for qb in chunk:
                     counts[bi, qb, hi] = int(sel[bi, qb, hi].sum())

@@ -16,7 +16,7 @@ import os
 import torch
 
 BLOCK = 64
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -39,12 +39,13 @@ _SIGNATURES = {
     "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64,
                            _p, _p, _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
-                           _p, _p, _p, _p, _p, _p, _int, _p], ctypes.c_int),
+                           _p, _p, _p, _p, _p, _p, _p, _p, _int, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
                        _dbl, _p, _p, _p], ctypes.c_int),
     "sol_plan_protection": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
     "sol_key_covariance_workspace_size": ([_i64, _i64, _i64], ctypes.c_int64),
     "sol_key_covariance": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "sol_quantize_keys": ([_p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "sol_attention_noalloc": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
                                _dbl, _dbl, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
 }
@@ -126,7 +127,7 @@ def _region(ws, offset, dtype, shape):
     return ws[offset:offset + n].view(dtype).view(shape)
 
 
-def pool_kv(k, v, key_index=None, moments=True, key_lengths=None, stream=None, views=True):
+def pool_kv(k, v, key_index=None, moments=True, key_lengths=None, stream=None, views=True, qk_int8=False):
     """Centroid tiles, attention tiles and key moments (one HBM pass over K and V).
 
     ``k``/``v``: ``[B, Tk, H, D]`` BF16 or, with ``key_index`` ``[B, Tk]``,
@@ -136,7 +137,8 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None, stream=None, v
     the buffers' device addresses (``*_ptr``) and, with ``views``, tensor views
     ``ctiles`` ``[B, H, NCT, 2, 64 D]`` (block centroids), ``tiles``
     ``[B, H, NKB, 2, 64 D]`` and ``mean``/``var`` ``[B, H, D]`` (None without
-    ``moments``); layouts per ``include/sol_attn_amd.h``.
+    ``moments``); layouts per ``include/sol_attn_amd.h``.  ``qk_int8`` also
+    quantises the K tiles (``sol_quantize_keys``) for the INT8-QK experiment.
     """
     lib = library()
     indexed = key_index is not None
@@ -153,19 +155,26 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None, stream=None, v
         stream = _stream(dev)
     tile = 2 * BLOCK * d * 2  # bytes of one K/V tile pair
     sizes = [b * h * nct * tile, b * h * nkb * tile]
-    if moments:
-        sizes += [b * h * -(-nkb // 16) * 2 * d * 4, b * h * d * 4, b * h * d * 4]
+    sizes += [b * h * -(-nkb // 16) * 2 * d * 4, b * h * d * 4, b * h * d * 4] if moments else [0, 0, 0]
+    if qk_int8:
+        sizes += [b * h * nkb * BLOCK * d, b * h * nkb * 4]
     offsets, total = _carve(sizes)
     ws = torch.empty(total, device=dev, dtype=torch.uint8)
     base = ws.data_ptr()
     ctiles, tiles = base + offsets[0], base + offsets[1]
-    sums, mean, var = (base + o for o in offsets[2:]) if moments else (None, None, None)
+    sums, mean, var = (base + o for o in offsets[2:5]) if moments else (None, None, None)
     _check(lib.sol_pool_kv(k.data_ptr(), _strides(k, indexed), v.data_ptr(), _strides(v, indexed),
                            _ptr(key_index), _ptr(key_lengths), k.shape[0] if indexed else 0,
                            b, tk, h, d, ctiles, tiles, sums, mean, var, stream))
     pooled = {"workspace": ws, "shape": (b, h, d), "ctiles_ptr": ctiles, "tiles_ptr": tiles,
               "mean_ptr": mean, "var_ptr": var, "cov_ptr": None, "key_tokens": tk,
-              "key_blocks": nkb, "key_lengths": key_lengths}
+              "key_blocks": nkb, "key_lengths": key_lengths, "k8_ptr": None, "k8_scale_ptr": None}
+    if qk_int8:
+        k8, k8s = base + offsets[5], base + offsets[6]
+        _check(lib.sol_quantize_keys(tiles, b, tk, h, d, k8, k8s, stream))
+        pooled["k8_ptr"], pooled["k8_scale_ptr"] = k8, k8s
+        if views:
+            pooled["k8_scale"] = _region(ws, offsets[6], torch.float32, (b, h, nkb))
     if views:
         pooled["ctiles"] = _region(ws, offsets[0], torch.bfloat16, (b, h, nct, 2, BLOCK * d))
         pooled["tiles"] = _region(ws, offsets[1], torch.bfloat16, (b, h, nkb, 2, BLOCK * d))
@@ -281,7 +290,7 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
         _ptr(prot), _ptr(strides), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
         out.data_ptr(), _ptr(rows if scatter else None), _ptr(counts),
         _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
-        WORKGROUP_FORM, stream))
+        pooled["k8_ptr"], pooled["k8_scale_ptr"], WORKGROUP_FORM, stream))
     if debug:
         dbg["selected"] = dbg["selected"].bool()
     return out, counts, dbg
@@ -289,20 +298,22 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
 
 def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=None,
                rows=None, keys=None, debug=False, key_lengths=None, out=None,
-               threshold_estimator="diagonal_covariance"):
+               threshold_estimator="diagonal_covariance", qk_precision="bf16"):
     """All-in SOL attention (``kernels.py:203-225``): pooling, moments, routing, attention.
 
     ``rows``/``keys`` (indexed windows) gather Q and K/V token rows inside the
     kernels instead of materialising copies; ``key_lengths`` makes the windows'
     key counts ragged and ``out`` scatters the result rows (see :func:`attend`).
     ``threshold_estimator="full_covariance"`` builds the cutoff from the full
-    key covariance (:func:`key_covariance`) instead of its diagonal.
+    key covariance (:func:`key_covariance`) instead of its diagonal;
+    ``qk_precision="int8"`` runs the exact blocks' scores on INT8 (queries
+    per row, keys per block; the INT8-QK experiment).
     Returns ``(out, counts)`` (``counts`` None unless ``stats``) and, with
     ``debug=True``, a dict of routing diagnostics as a third element.
     """
     stream = _stream(q.device)
     pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths,
-                     stream=stream, views=debug)
+                     stream=stream, views=debug, qk_int8=qk_precision == "int8")
     if threshold_estimator == "full_covariance" and not math.isinf(beta):
         key_covariance(pooled, stream)
     out, counts, dbg = attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection, rows,

@@ -94,9 +94,18 @@ def _threshold_estimator(name):
     return name
 
 
+QK_PRECISIONS = ("bf16", "int8")
+
+
+def _qk_precision(name):
+    if name not in QK_PRECISIONS:
+        raise ValueError("qk_precision must be 'bf16' or 'int8'")
+    return name
+
+
 def sol_attention(q, k, v, *, beta=1.0, scale=None, local_blocks=1,
                   kv_sink_tokens=0, query_sink_tokens=0, return_stats=False,
-                  threshold_estimator="diagonal_covariance"):
+                  threshold_estimator="diagonal_covariance", qk_precision="bf16"):
     """SOL-style noncausal attention (``attention.py:58-85``).
 
     Physical blocks hold 64 tokens.  Selected blocks use BF16 QK/PV with FP32
@@ -111,12 +120,19 @@ def sol_attention(q, k, v, *, beta=1.0, scale=None, local_blocks=1,
     ``sqrt(sum Qc^2 var)`` with ``sqrt(max(Qc^T cov Qc, 0))`` over the full
     covariance of the key centroids; the default keeps the reference's
     diagonal estimator.
+
+    ``qk_precision="int8"`` (not in the reference: the INT8-QK experiment of
+    its roadmap) computes the selected blocks' scores as ``s_q s_k (Q8 . K8)``
+    on the INT8 matrix cores -- each query row quantised with one symmetric
+    scale, each 64-key block of K with one -- while routing, the centroid
+    terms and the P V product stay BF16.  The default keeps BF16 scores.
     """
     scale = _validate(q, k, v, scale)
     beta = float(beta)
     if math.isnan(beta):
         raise ValueError("beta must not be NaN")
     _threshold_estimator(threshold_estimator)
+    _qk_precision(qk_precision)
     for name, value in (("local_blocks", local_blocks),
                         ("kv_sink_tokens", kv_sink_tokens),
                         ("query_sink_tokens", query_sink_tokens)):
@@ -128,7 +144,7 @@ def sol_attention(q, k, v, *, beta=1.0, scale=None, local_blocks=1,
     with torch.no_grad(), torch.cuda.device(q.device):
         out, counts = launch_sol(q, k, v, scale, beta, local_blocks,
                                  kv_sink_tokens, query_sink_tokens, return_stats,
-                                 threshold_estimator=threshold_estimator)
+                                 threshold_estimator=threshold_estimator, qk_precision=qk_precision)
     if return_stats:
         return out, SolStats(counts, (k.shape[1] + 63) // 64)
     return out

@@ -168,6 +168,82 @@ __device__ __forceinline__ void centroid_tile(State<D>& st, const uint16_t* buf,
                        refill);
 }
 
+// The quantised-QK experiment's exact tile: S^T = K8 Q8^T on the INT8 matrix
+// cores (D / 32 products per 32-key half instead of D / 16), then the INT32
+// scores converted to FP32 and scaled inside the softmax by c8 = c s_q s_k
+// (the lane's query scale, the tile's key scale); absent keys of the tail
+// block (TAIL) start at -inf.  The softmax and O^T += V^T P^T are those of
+// tile_attend, with the same in-wave interleave: half 0's products; half
+// 1's products with half 0's softmax and V^T reads; half 0's P V with half
+// 1's softmax; half 1's P V.  The refill's DMA rounds are spread over the
+// 2 D / 32 score chunks.
+template <int D, bool TAIL, typename Refill>
+__device__ __forceinline__ void tile_attend_i8(State<D>& st, const uint16_t* buf, const i32x4 (&q8)[D / 32],
+                                               int col, int hh, float c8, int lane_keys, const Refill& refill) {
+  constexpr int K8 = D / 32, DT = Shape<D>::DT;
+  static_assert(K8 == DT, "two V^T fragments of half 0 per score chunk");
+  const FragLane<D> fl(fresh(col), fresh(hh));
+  const int8_t* kbuf = reinterpret_cast<const int8_t*>(buf);
+  const int c0 = fresh(col);
+  const int krow = c0 * D;                                 // row col of the K8 tile
+  const int kx = 16 * (fresh(hh) ^ K8Layout<D>::swizzle(c0));  // chunk 2 ks8 + hh at kx ^ 32 ks8
+  auto kfrag = [&](int t, int ks8) {
+    return *reinterpret_cast<const i32x4*>(kbuf + krow + 32 * t * D + (kx ^ (32 * ks8)));
+  };
+  auto to_scores = [&](const i32x16& x, int t) {
+    f32x16 sc;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      sc[e] = float(x[e]);
+      if (TAIL && tile_row(t, e, 0) >= lane_keys) sc[e] = kNegInf;
+    }
+    return sc;
+  };
+  i32x4 k0[K8], k1[K8];
+#pragma unroll
+  for (int ks = 0; ks < K8; ++ks) k0[ks] = kfrag(0, ks);
+  HalfSoftmax<D> h0, h1;
+  i32x16 i0, i1;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) i0[e] = i1[e] = 0;
+  chunk_end();
+#pragma unroll
+  for (int ks = 0; ks < K8; ++ks) {
+    i0 = mfma32x32x32i8(k0[ks], q8[ks], i0);
+    k1[ks] = kfrag(1, ks);
+    refill.template after_step<2 * K8>(ks);
+    chunk_end();
+  }
+  u32x4 va[2][DT];
+#pragma unroll
+  for (int ks = 0; ks < K8; ++ks) {
+    i1 = mfma32x32x32i8(k1[ks], q8[ks], i1);
+    if (ks == 0) h0.s = to_scores(i0, 0);
+    h0.template part<K8>(ks, st, c8);
+#pragma unroll
+    for (int f = 2 * ks; f < 2 * ks + 2; ++f) va[f / DT][f % DT] = fl.v(buf, 0, f / DT, f % DT);
+    refill.template after_step<2 * K8>(K8 + ks);
+    chunk_end();
+  }
+  if (h0.rescale) rescale_acc<D>(st, h0.alpha);
+  u32x4 vb[2][DT];
+#pragma unroll
+  for (int f = 0; f < 2 * DT; ++f) {
+    const int c4 = f / DT, dt = f % DT;
+    st.acc[dt] = mfma32x32x16(as_bf16x8(va[c4][dt]), h0.pb(c4), st.acc[dt]);
+    vb[c4][dt] = fl.v(buf, 1, c4, dt);
+    if (f == 0) h1.s = to_scores(i1, 1);
+    h1.template part<2 * DT>(f, st, c8);
+    chunk_end();
+  }
+  if (h1.rescale) rescale_acc<D>(st, h1.alpha);
+#pragma unroll
+  for (int f = 0; f < 2 * DT; ++f) {
+    const int c4 = f / DT, dt = f % DT;
+    st.acc[dt] = mfma32x32x16(as_bf16x8(vb[c4][dt]), h1.pb(c4), st.acc[dt]);
+  }
+}
+
 // Waits until at most `ahead` tiles' DMA (the newest ones) are still in flight.
 template <int kRounds>
 __device__ __forceinline__ void wait_ahead(int ahead) {
@@ -196,8 +272,9 @@ __device__ __forceinline__ void wait_ahead(int ahead) {
 // only the common case (an exact stream's last tile may be a partial
 // block).  `next()` yields tile references (ids, or tags that carry an
 // id) in order; the tile each reference names is the same for every thread,
-// while selected(ref) may differ between waves.  source(ref) is the tile's
-// HBM address.  R = 1: one slot, refilled after a barrier (latency
+// while selected(ref) may differ between waves.  make(ref, lds) returns the
+// refill (TileRefill, Q8Refill) that DMAs tile ref into the LDS slot at lds.
+// R = 1: one slot, refilled after a barrier (latency
 // hidden by the other workgroups of the CU).  Two streams over the same ring
 // are separated by a barrier.
 // Selection predicate and the two tile consumers of a stream.
@@ -213,11 +290,17 @@ __device__ __forceinline__ TileRuns<Sel, Hit, Miss> tile_runs(Sel selected, Hit 
   return {selected, hit, miss};
 }
 
-template <int D, int NT, int R, typename Next, typename Source, typename Runs, typename Last>
-__device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next, Source source,
+// Refill factory for BF16 tile pairs at HBM address source(ref).
+template <int D, int NT, typename Source>
+__device__ __forceinline__ auto bf16_refills(Source source, int wave, int lane) {
+  return [=](int ref, uint32_t lds) { return TileRefill<D, NT>(source(ref), lds, wave, lane); };
+}
+
+template <int D, int NT, int R, typename Next, typename Make, typename Runs, typename Last>
+__device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next, Make make,
                                             Runs runs, Last last, int wave, int lane) {
   using S = Shape<D>;
-  constexpr int kRounds = S::TILE / 8 / NT;
+  constexpr int kRounds = decltype(make(0, 0u))::kRounds;
   static_assert(R >= 1 && R <= 4 && (R & (R - 1)) == 0, "ring depth 1, 2 or 4");
   static_assert(R < 2 || (R - 2) * kRounds <= 63, "vmcnt range");
   if (count <= 0) return;
@@ -225,7 +308,7 @@ __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next
   if constexpr (R == 1) {
     for (int i = 0; i < count; ++i) {
       const int id = next();
-      TileRefill<D, NT>(source(id), ring_lds, wave, lane).all();
+      make(id, ring_lds).all();
       wait_vmcnt<0>();
       ring_barrier();
       if (i + 1 < count) {
@@ -245,7 +328,7 @@ __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next
 #pragma unroll
   for (int s = 0; s < R - 1; ++s) {
     ids[s] = s < count ? next() : 0;
-    if (s < count) tile_dma<D, NT>(source(ids[s]), ring_lds + uint32_t(s * S::TILE * 2), wave, lane);
+    if (s < count) make(ids[s], ring_lds + uint32_t(s * S::TILE * 2)).all();
   }
   auto step = [&](int i, auto&& fn) {
     wait_ahead<kRounds>(min(R - 2, count - 1 - i));
@@ -258,8 +341,7 @@ __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next
       idn = next();
       ids[R - 2] = idn;
     }
-    fn(ring + (i & (R - 1)) * S::TILE, id,
-       TileRefill<D, NT>(source(idn), ring_lds + uint32_t(((i + R - 1) & (R - 1)) * S::TILE * 2), wave, lane));
+    fn(ring + (i & (R - 1)) * S::TILE, id, make(idn, ring_lds + uint32_t(((i + R - 1) & (R - 1)) * S::TILE * 2)));
   };
   int i = 0;
   while (i < count - 1) {
@@ -339,7 +421,7 @@ struct RangeCursor {
 // The bound names 256 threads for both workgroup forms, so the one-block form
 // (128 threads) is held to the same budget (with its own 128-thread bound the
 // compiler moves values through AGPRs instead).
-template <int D, int G, int R>
+template <int D, int G, int R, bool Q8>
 __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   using S = Shape<D>;
   using TL = TileLayout<D>;
@@ -388,6 +470,45 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
 #pragma unroll
     for (int ks = 0; ks < S::KT; ++ks)
       qf[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qrow + ks * 16 + 8 * hh));
+  }
+  // Quantised-QK experiment: the query row as INT8 with one symmetric scale
+  // s_q = max|q| / 127 (round to nearest even, clamped to +-127).  The lane
+  // holds features 32 ks8 + 16 hh .. +15 of product ks8, as the K8 tile rows do.
+  i32x4 q8[Q8 ? D / 32 : 1];
+  float csq = 0.f;  // c s_q
+  if constexpr (Q8) {
+    const uint16_t* qrow = ring + (qg * kBlock + myq) * S::KS;
+    u32x4 raw[D / 32][2];
+    float amax = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        raw[ks][hf] = *reinterpret_cast<const u32x4*>(qrow + 32 * ks + 16 * hh + 8 * hf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t w = raw[ks][hf][e >> 1];
+          amax = fmaxf(amax, fabsf(bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu))));
+        }
+      }
+    amax = pair_max(amax);
+    const float inv = amax > 0.f ? __fdiv_rn(127.f, amax) : 0.f;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks)
+#pragma unroll
+      for (int wd = 0; wd < 4; ++wd) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int bt = 0; bt < 4; ++bt) {
+          const int e = 4 * wd + bt;  // feature 32 ks + 16 hh + e
+          const uint32_t w = raw[ks][e >> 3][(e & 7) >> 1];
+          const float x = bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu));
+          const int qi = int(fminf(fmaxf(rintf(__fmul_rn(x, inv)), -127.f), 127.f));
+          packed |= (uint32_t(qi) & 0xFFu) << (8 * bt);
+        }
+        q8[ks][wd] = int32_t(packed);
+      }
+    csq = p.scale_log2 * __fdiv_rn(amax, 127.f);
   }
 
   // 2. Query mean and cutoff per query block (sums in torch's cascade order).
@@ -501,7 +622,7 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
     };
     auto always = [](int) { return true; };
     tile_stream<D, NT, R>(ring, nct, RangeCursor{0},
-                          [&](int ct) { return ctiles + int64_t(ct) * S::TILE; },
+                          bf16_refills<D, NT>([=](int ct) { return ctiles + int64_t(ct) * S::TILE; }, wave, lane),
                           tile_runs(always, process, process), process, wave, lane);
     lds_barrier();  // every wave is done with the ring's centroid tiles
   }
@@ -518,21 +639,52 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   const int count = cursor.count();
   const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
   auto selected = [](int tag) { return (tag & 1) != 0; };
-  auto hit = [&](const uint16_t* buf, int, const auto& refill) {
-    full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
-  };
   auto miss = [&](const uint16_t*, int, const auto& refill) { refill.all(); };
-  tile_stream<D, NT, R>(
-      ring, count, cursor, [&](int tag) { return tiles + int64_t(tag >> 1) * S::TILE; },
-      tile_runs(selected, hit, miss),
-      [&](const uint16_t* buf, int tag, const auto& refill) {
-        if (tag & 1) {
-          exact_tile<D>(st, buf, tag >> 1, tk, qf, col, hh, scale_log2, refill);
-        } else {
-          refill.all();
-        }
-      },
-      wave, lane);
+  if constexpr (!Q8) {
+    auto hit = [&](const uint16_t* buf, int, const auto& refill) {
+      full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
+    };
+    tile_stream<D, NT, R>(
+        ring, count, cursor, bf16_refills<D, NT>([=](int tag) { return tiles + int64_t(tag >> 1) * S::TILE; },
+                                                 wave, lane),
+        tile_runs(selected, hit, miss),
+        [&](const uint16_t* buf, int tag, const auto& refill) {
+          if (tag & 1) {
+            exact_tile<D>(st, buf, tag >> 1, tk, qf, col, hh, scale_log2, refill);
+          } else {
+            refill.all();
+          }
+        },
+        wave, lane);
+  } else {
+    // Quantised QK: INT8 K tiles and their scales (the V^T halves still come
+    // from the BF16 tile pairs).
+    const int8_t* k8 = p.k8 + head * p.NKB * K8Layout<D>::kBytes;
+    const float* k8s = p.k8_scale + head * p.NKB;
+    auto make = [=](int tag, uint32_t lds) {
+      const int64_t j = tag >> 1;
+      return Q8Refill<D, NT>(k8 + j * K8Layout<D>::kBytes, tiles + j * S::TILE + TileLayout<D>::kElems, lds,
+                             wave, lane);
+    };
+    auto hit = [&](const uint16_t* buf, int tag, const auto& refill) {
+      tile_attend_i8<D, false>(st, buf, q8, col, hh, csq * k8s[tag >> 1], 0, refill);
+    };
+    tile_stream<D, NT, R>(
+        ring, count, cursor, make, tile_runs(selected, hit, miss),
+        [&](const uint16_t* buf, int tag, const auto& refill) {
+          if (tag & 1) {
+            const int j = tag >> 1;
+            const float c8 = csq * k8s[j];
+            if ((j + 1) * kBlock <= tk)
+              tile_attend_i8<D, false>(st, buf, q8, col, hh, c8, 0, refill);
+            else
+              tile_attend_i8<D, true>(st, buf, q8, col, hh, c8, fresh(tk - j * kBlock - 4 * hh), refill);
+          } else {
+            refill.all();
+          }
+        },
+        wave, lane);
+  }
 
   // 5. Normalise and store.
   if (live) store_output<D>(p, b, h, qb * kBlock + myq, hh, st);
@@ -583,7 +735,7 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
     full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
   };
   tile_stream<D, NT, 2>(
-      ring, p.NKB, RangeCursor{0}, [&](int j) { return tiles + int64_t(j) * S::TILE; },
+      ring, p.NKB, RangeCursor{0}, bf16_refills<D, NT>([=](int j) { return tiles + int64_t(j) * S::TILE; }, wave, lane),
       tile_runs(always, hit, hit),
       [&](const uint16_t* buf, int j, const auto& refill) {
         exact_tile<D>(st, buf, j, tk, qf, col, hh, scale_log2, refill);
@@ -607,7 +759,10 @@ void launch_sol_group(const AttnParams& p, hipStream_t stream) {
   // Grid of sol_task: the sink-holding tiles of every head, then xcd_task's.
   const int ntiles = (p.NQB + G - 1) / G, front = std::min(p.q_sink_blocks, ntiles);
   const unsigned grid = unsigned(front) * unsigned(p.B * p.H) + xcd_grid(p.B * p.H, ntiles - front);
-  hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing>), dim3(grid), dim3(128 * G), 0, stream, p);
+  if (p.k8)
+    hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, true>), dim3(grid), dim3(128 * G), 0, stream, p);
+  else
+    hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, false>), dim3(grid), dim3(128 * G), 0, stream, p);
 }
 
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {

@@ -174,6 +174,50 @@ struct TileRefill {
   }
 };
 
+// DMA of the quantised-QK experiment's tiles into one LDS slot: the INT8 K
+// tile of a key block (64 rows x D bytes, from the INT8 tile array) at the
+// slot's start, then the V^T half of its BF16 tile pair at the V^T offset
+// of the BF16 layout (so the P V operand reads are unchanged).  Rounds as in
+// TileRefill: the K8 rounds first, then the V^T rounds.
+template <int D, int NT>
+struct Q8Refill {
+  static constexpr int kK8Rounds = kBlock * D / 16 / NT;
+  static constexpr int kVRounds = kBlock * D * 2 / 16 / NT;
+  static constexpr int kRounds = kK8Rounds + kVRounds;
+  static_assert(kK8Rounds * NT * 16 == kBlock * D, "INT8 tile must split evenly over the workgroup");
+  uint64_t k8src, vsrc;
+  uint32_t lds;
+  uint32_t lane_bytes;
+
+  __device__ __forceinline__ Q8Refill(const int8_t* k8tile, const uint16_t* vt, uint32_t dst_lds, int wave,
+                                      int lane)
+      : k8src(uniform64(reinterpret_cast<uint64_t>(k8tile) + uint64_t(wave) * (kWave * 16))),
+        vsrc(uniform64(reinterpret_cast<uint64_t>(vt) + uint64_t(wave) * (kWave * 16))),
+        lds(uint32_t(__builtin_amdgcn_readfirstlane(dst_lds + uint32_t(wave) * (kWave * 16)))),
+        lane_bytes(uint32_t(lane) * 16u) {}
+
+  __device__ __forceinline__ void round(int r) const {
+    if (r < kK8Rounds) {
+      uint32_t off = uint32_t(r) * (NT * 16);
+      asm volatile("" : "+s"(off));
+      dma16(k8src + off, lane_bytes, lds + off);
+    } else {
+      uint32_t off = uint32_t(r - kK8Rounds) * (NT * 16);
+      asm volatile("" : "+s"(off));
+      dma16(vsrc + off, lane_bytes, lds + uint32_t(TileLayout<D>::kElems * 2) + off);
+    }
+  }
+  __device__ __forceinline__ void all() const {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) round(r);
+  }
+  template <int N>
+  __device__ __forceinline__ void after_step(int k) const {
+#pragma unroll
+    for (int r = k * kRounds / N; r < (k + 1) * kRounds / N; ++r) round(r);
+  }
+};
+
 // A refill with nothing to load (single-slot ring).
 struct NoRefill {
   __device__ __forceinline__ void all() const {}

@@ -262,6 +262,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
+                      const void* qk_int8_tiles, const float* qk_int8_scales,
                       int workgroup_form, void* stream) {
   if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
       key_tokens >= (int64_t(1) << 30))
@@ -272,6 +273,10 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_index / out_index need sequence_length > 0");
   if (workgroup_form < 0 || workgroup_form > 3)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: workgroup_form must be 0, 1, 2 or 3");
+  if ((qk_int8_tiles == nullptr) != (qk_int8_scales == nullptr) || (qk_int8_tiles && !aligned16(qk_int8_tiles)))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: qk_int8_tiles (16-byte aligned) and qk_int8_scales go together");
+  if (qk_int8_tiles && workgroup_form == 3)
+    return fail(SOL_ERR_UNSUPPORTED, "sol_attention_fwd: the INT8 QK experiment runs in workgroup forms 0, 1 and 2");
   if (!std::isfinite(scale) || scale <= 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: scale must be finite and positive");
   if (std::isnan(beta)) return fail(SOL_ERR_INVALID, "sol_attention_fwd: beta must not be NaN");
@@ -296,6 +301,8 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   p.out_index = out_index;
   p.out_rows = sequence_length;
   p.workgroup_form = workgroup_form;
+  p.k8 = static_cast<const int8_t*>(qk_int8_tiles);
+  p.k8_scale = qk_int8_scales;
   p.tiles = static_cast<const uint16_t*>(tiles);
   p.ctiles = static_cast<const uint16_t*>(ctiles);
   p.mean = key_mean;
@@ -323,6 +330,22 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   p.kv_sink_blocks = int(cdiv(kv_sink_tokens > big ? big : kv_sink_tokens, SOL_BLOCK));
   p.q_sink_blocks = int(cdiv(query_sink_tokens > big ? big : query_sink_tokens, SOL_BLOCK));
   return hip_status(sol::launch_sol(p, int(head_dim), static_cast<hipStream_t>(stream)));
+}
+
+int sol_quantize_keys(const void* tiles, int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
+                      void* k8_tiles, float* k8_scales, void* stream) {
+  if (!shape_ok(batch, key_tokens, heads, head_dim))
+    return fail(SOL_ERR_INVALID, "sol_quantize_keys: unsupported shape (head_dim must be 64 or 128)");
+  if (!tiles || !k8_tiles || !k8_scales || !aligned16(tiles) || !aligned16(k8_tiles))
+    return fail(SOL_ERR_INVALID, "sol_quantize_keys: tiles and k8_tiles (16-byte aligned) and k8_scales are required");
+  const int64_t ntiles = batch * heads * cdiv(key_tokens, SOL_BLOCK);
+  if (ntiles >= (int64_t(1) << 31)) return fail(SOL_ERR_UNSUPPORTED, "sol_quantize_keys: grid too large");
+  sol::QuantParams p;
+  p.tiles = static_cast<const uint16_t*>(tiles);
+  p.k8 = static_cast<int8_t*>(k8_tiles);
+  p.scale = k8_scales;
+  p.ntiles = ntiles;
+  return hip_status(sol::launch_quantize_keys(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
 int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
@@ -393,7 +416,7 @@ int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k
   return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
                            head_dim, ws + off_tiles, ws, mean, var, nullptr, nullptr, nullptr, scale, beta,
                            local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr, counts, nullptr,
-                           nullptr, nullptr, 0, stream);
+                           nullptr, nullptr, nullptr, nullptr, 0, stream);
 }
 
 }  // extern "C"

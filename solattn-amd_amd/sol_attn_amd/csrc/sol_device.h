@@ -53,6 +53,16 @@ __device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// 32x32x32 INT8 products, INT32 accumulation.  Operand lane layout as the
+// BF16 32x32x16 form, with 16 INT8 k-slots per lane (k-slots 16 (l / 32) ..
+// +15); the C/D layout is the same.
+__device__ __forceinline__ i32x16 mfma32x32x32i8(i32x4 a, i32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ f32x16 zero16() {
@@ -188,6 +198,18 @@ struct TileLayout {
   __device__ static __forceinline__ int vt_offset(int d, int g) {
     return vt_chunk(d, 2 * (g >> 2) + (g & 1)) + 4 * ((g >> 1) & 1);
   }
+};
+
+// INT8 K tiles of the quantised-QK experiment: per key block 64 rows x D
+// bytes; 16-byte chunk c (features 16 c .. 16 c + 15) of row r sits at chunk
+// c ^ s8(r), s8(r) = (r >> 1) & 7 for 128-byte rows (D = 128) and (r >> 2) & 3
+// for 64-byte rows (D = 64): the 16 rows of one ds_read_b128 phase then cover
+// all 64 banks.  One FP32 scale per block: K = scale * K8.
+template <int D>
+struct K8Layout {
+  static constexpr int kBytes = kBlock * D;
+  __device__ static __forceinline__ int swizzle(int row) { return D == 128 ? ((row >> 1) & 7) : ((row >> 2) & 3); }
+  __device__ static __forceinline__ int offset(int row, int chunk) { return row * D + 16 * (chunk ^ swizzle(row)); }
 };
 
 }  // namespace sol

@@ -64,6 +64,8 @@ struct AttnParams {
   const float* mean;           // [B, H, D]
   const float* var;            // [B, H, D]
   const float* cov;            // [B, H, D, D] full key covariance, or null: diagonal (var)
+  const int8_t* k8;            // [B, H, NKB, 64 * D] INT8 K tiles (quantised-QK experiment), or null
+  const float* k8_scale;       // [B, H, NKB] their scales
   const uint8_t* protection;   // [B, NQB, NKB] or null
   uint16_t* out;               // [B, Tq, H, D], or [N, H, D] rows out_index
   int32_t* counts;             // [B, NQB, H] or null
@@ -90,7 +92,16 @@ struct PlanParams {
   int nranges;
 };
 
+// INT8 K tiles of the quantised-QK experiment (quant.hip).
+struct QuantParams {
+  const uint16_t* tiles;  // [B, H, NKB, 2, 64 * D] BF16 tile pairs (K halves read)
+  int8_t* k8;             // [B, H, NKB, 64 * D]
+  float* scale;           // [B, H, NKB]
+  int64_t ntiles;         // B * H * NKB
+};
+
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream);
+hipError_t launch_quantize_keys(const QuantParams& p, int D, hipStream_t stream);
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_sol_pp(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_dense_pp(const AttnParams& p, int D, hipStream_t stream);

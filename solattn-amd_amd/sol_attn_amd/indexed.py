@@ -18,7 +18,8 @@ import math
 
 import torch
 
-from .attention import SolStats, _key_length, _validate, _nonnegative_integer, _threshold_estimator
+from .attention import (SolStats, _key_length, _validate, _nonnegative_integer, _qk_precision,
+                        _threshold_estimator)
 
 BLOCK = 64
 
@@ -155,7 +156,7 @@ class IndexedPlan:
 
 
 def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=False, out=None,
-                          threshold_estimator="diagonal_covariance"):
+                          threshold_estimator="diagonal_covariance", qk_precision="bf16"):
     """BF16 NHD inputs -> ``[windows, query_rows, heads, D]`` (``indexed.py:69-104``).
 
     Window ``w`` attends its query rows ``plan.rows[w]`` to its keys
@@ -173,7 +174,7 @@ def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=F
     rows outside it, so a plan whose tensors were changed after ``create``
     cannot make them access memory outside Q/K/V or ``out``.
 
-    ``threshold_estimator``: as in :func:`sol_attention`.
+    ``threshold_estimator``, ``qk_precision``: as in :func:`sol_attention`.
     """
     if any(t.ndim != 3 for t in (q, k, v)) or q.shape != k.shape or k.shape != v.shape:
         raise ValueError("Indexed Q/K/V must have matching NHD shapes")
@@ -207,12 +208,13 @@ def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=F
     if math.isnan(beta):
         raise ValueError("beta must not be NaN")
     _threshold_estimator(threshold_estimator)
+    _qk_precision(qk_precision)
     from ._native import launch_sol
     with torch.no_grad(), torch.cuda.device(q.device):
         result, counts = launch_sol(q, k, v, scale, beta, -1, 0, 0, return_stats,
                                     plan.protected_blocks, rows=plan.rows, keys=plan.keys,
                                     key_lengths=lengths, out=out,
-                                    threshold_estimator=threshold_estimator)
+                                    threshold_estimator=threshold_estimator, qk_precision=qk_precision)
     if return_stats:
         key_blocks = ((plan.keys.shape[1] + 63) // 64 if lengths is None
                       else (lengths.to(torch.int64) + 63) // 64)

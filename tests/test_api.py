@@ -144,7 +144,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == 6
+    assert native.sol_abi_version() == 7
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -168,10 +168,10 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     assert rc == -1 and b"scale" in native.sol_last_error()
     attn = lambda index, n, form: native.sol_attention_fwd(  # noqa: E731
         fake, strides, index, n, 1, 193, 317, None, 2, 64, fake, fake, fake, fake, None, None, None,
-        0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, form, None)
+        0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, form, None)
     rc = native.sol_attention_fwd(fake, strides, None, 0, 1, 193, 317, None, 2, 64, fake, fake,
                                   None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None,
-                                  None, None, None, 0, None)
+                                  None, None, None, None, None, 0, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
     assert attn(None, 0, 4) == -1 and b"workgroup_form" in native.sol_last_error()
     assert attn(fake, 0, 0) == -1 and b"sequence_length" in native.sol_last_error()

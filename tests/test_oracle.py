@@ -292,6 +292,80 @@ def test_full_covariance_beta_zero_and_oracle_option():
         orc.sol_oracle(q, k, v, threshold_estimator="banded")
 
 
+def test_int8_quantisation_closed_forms():
+    # Round half to even, clamp, the scale, and an all-zero group.
+    x = np.array([[0.5, 1.5, -2.5, 127.0], [0.0, 0.0, 0.0, 0.0], [254.0, -1.0, 63.5, 127.5]], np.float32)
+    q, sc = orc.quantize_sym(x, axes=1)
+    np.testing.assert_array_equal(q[0], [0, 2, -2, 127])       # amax 127: q = rint(x)
+    np.testing.assert_array_equal(q[1], [0, 0, 0, 0])
+    np.testing.assert_array_equal(sc[:, 0], np.float32([1.0, 0.0, 2.0]))
+    np.testing.assert_array_equal(q[2], [127, -0, 32, 64])      # x / 2: 31.75 -> 32, 63.75 -> 64
+    k = np.zeros((1, 70, 1, 16), np.float32)
+    k[0, 3, 0, 5] = -4.0                                        # block 0's max; block 1 is 6 rows
+    k[0, 64:, 0, :] = 1.0
+    k8, sk = orc.quantize_keys(k)
+    assert k8.shape == k.shape and sk.shape == (1, 2, 1)
+    np.testing.assert_array_equal(sk[0, :, 0], np.float32([4.0 / 127, 1.0 / 127]))
+    assert k8[0, 3, 0, 5] == -127 and (k8[0, 64:] == 127).all()
+
+
+def test_int8_oracle_equals_bf16_oracle_on_the_int8_grid():
+    # Integer-valued Q and K whose every row / key block reaches |127| quantise
+    # exactly (scale 1), so the INT8-QK oracle must reproduce the BF16 one bit
+    # for bit; any other input it must not (pins the quantised path).
+    rng = np.random.default_rng(8)
+    q = rng.integers(-126, 127, (1, 150, 2, 64)).astype(np.float32)
+    k = rng.integers(-126, 127, (1, 200, 2, 64)).astype(np.float32)
+    q[..., 0] = 127.0
+    k[..., 0] = -127.0
+    v = orc.bf16_round(rng.standard_normal((1, 200, 2, 64)).astype(np.float32))
+    scale = 1.0 / 4096
+    for beta in (1.0, -math.inf, 0.0):
+        a, ca, _ = orc.sol_oracle(q, k, v, beta=beta, scale=scale)
+        b, cb, _ = orc.sol_oracle(q, k, v, beta=beta, scale=scale, qk_precision="int8")
+        np.testing.assert_array_equal(a, b)
+        np.testing.assert_array_equal(ca, cb)
+    c, _, _ = orc.sol_oracle(q * 1.37, k, v, beta=1.0, scale=scale, qk_precision="int8")
+    d, _, _ = orc.sol_oracle(q * 1.37, k, v, beta=1.0, scale=scale)
+    assert not np.array_equal(c, d)
+
+
+def test_quantised_pv_accuracy_against_bf16_control():
+    """The FP8 P V half of the roadmap experiment, in simulation: the
+    probabilities rounded to FP8-e4m3 (with V kept BF16, or V also FP8)
+    instead of BF16, float64 elsewhere, against the BF16-P control.  On
+    random inputs FP8 P leaves the parity bar (rel-L2 0.8%); on block-smooth
+    inputs it stays inside it."""
+    rng = np.random.default_rng(1)
+    t, d = 1024, 128
+
+    def fp8(x):
+        return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(torch.float8_e4m3fn).float().numpy()
+
+    def attn(q, k, v, pq, pv):
+        s = q.astype(np.float64) @ k.T.astype(np.float64) / math.sqrt(d)
+        p = np.exp(s - s.max(1, keepdims=True))
+        return (pq(p) @ pv(v)) / p.sum(1, keepdims=True)
+
+    bf = lambda x: orc.bf16_round(np.asarray(x, np.float32))  # noqa: E731
+    ident = lambda x: x  # noqa: E731
+
+    def smooth():
+        c = rng.standard_normal((t // 64, d))
+        return bf(np.repeat(c, 64, 0) + 0.1 * rng.standard_normal((t, d)))
+
+    errs = {}
+    for name, make in (("random", lambda: bf(rng.standard_normal((t, d)))), ("smooth", smooth)):
+        q, k, v = make(), make(), make()
+        ref = attn(q, k, v, bf, ident)
+        for label, pq, pv in (("fp8p_bf16v", fp8, ident), ("fp8p_fp8v", fp8, fp8)):
+            o = attn(q, k, v, pq, pv)
+            errs[(name, label)] = np.linalg.norm(o - ref) / np.linalg.norm(ref)
+    assert 0.015 < errs[("random", "fp8p_bf16v")] < 0.04, errs
+    assert errs[("random", "fp8p_fp8v")] > errs[("random", "fp8p_bf16v")], errs
+    assert errs[("smooth", "fp8p_bf16v")] < 0.006 and errs[("smooth", "fp8p_fp8v")] < 0.008, errs
+
+
 def test_quantised_qk_accuracy_against_bf16_control():
     """The INT8 / FP8 QK half of the reference roadmap's experiment row, in
     simulation: attention with Q and K rounded to FP8-e4m3, or to INT8 with one
