@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 7
+#define SOL_ABI_VERSION 8
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
 
@@ -61,15 +61,18 @@ const char* sol_last_error(void);
  * calls of kernels.py:187,207,211-212), with NKB = ceil(key_tokens / 64) key
  * blocks and NCT = ceil(NKB / 64) centroid tiles:
  *   sizes[0] ctiles      bf16 [batch, heads, NCT, 2, 64 * head_dim]  block centroids
- *   sizes[1] tiles       bf16 [batch, heads, NKB, 2, 64 * head_dim]  K and V^T block tiles
+ *   sizes[1] tiles       bf16 [batch, heads, NKB, 2, 64 * head_dim]  K and V block tiles
  *   sizes[2] chunk_sums  fp32 [batch, heads, ceil(NKB/16), 2, head_dim]
  *   sizes[3] key_mean    fp32 [batch, heads, head_dim]  (key_var has the same size)
- * Tile pairs: a K tile (64 rows x head_dim) then a V^T tile (head_dim rows x 64),
- * bank-swizzled: 16-byte chunk c of K row r at chunk c ^ (r & 15) (head_dim 128)
- * or c ^ ((r >> 1) & 7) (head_dim 64).  A V^T row is 8 chunks of 16 bytes;
- * chunk c holds the 4-key groups 4 (c >> 1) + (c & 1) (low half) and that + 2
- * (high half), and sits at chunk c ^ (d & 7) ^ ((d >> 3) & 1) of row d.
- * Rows past the last key / block are zero. */
+ * Tile pairs: a K tile then a V tile, 64 rows x head_dim each, in 16-byte
+ * chunks (8 features): K chunk c of row r at chunk c ^ (r & 15) (head_dim 128)
+ * or c ^ ((r >> 1) & 7) (head_dim 64) of the row; V chunk c of row r at chunk
+ * (r >> 2) * head_dim / 2 + (c >> 2) * 16 + (r & 3) * 4 + (c & 3) of the tile
+ * (row quads).  Rows past the last key / block are zero.
+ * The block tiles are needed only when the attention kernels cannot read
+ * key blocks straight from K and V ("rows mode", see sol_attention_fwd):
+ * indexed or ragged keys, fewer than 64 keys, token strides of 2^24 elements
+ * or more. */
 int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
                    int64_t sizes[4]);
 
@@ -78,10 +81,10 @@ int sol_pool_sizes(int64_t batch, int64_t key_tokens, int64_t heads, int64_t hea
  * `_pool` kernels.py:16-27) and `_moments` (kernels.py:30-49).
  * sequence_length: rows key_index may address (ignored without key_index).
  * ctiles receives the BF16 (round-to-nearest-even) 64-token block means of K
- * and V (NULL: tiles only); tiles receives every key block as the tile pair the
- * attention kernels stream; when key_mean/key_var/chunk_sums are all
- * non-NULL, also the per-(batch, head, feature) population mean and clamped
- * variance of the BF16 key centroids. */
+ * and V (NULL: tiles only); tiles (NULL: none) receives every key block as the
+ * tile pair the attention kernels stream in tiles mode; when
+ * key_mean/key_var/chunk_sums are all non-NULL, also the per-(batch, head,
+ * feature) population mean and clamped variance of the BF16 key centroids. */
 int sol_pool_kv(const void* k, const int64_t* k_strides,
                 const void* v, const int64_t* v_strides,
                 const int64_t* key_index, const int32_t* key_lengths,
@@ -155,17 +158,21 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
  * experiment of the reference's roadmap (ROADMAP.md:14-16; not implemented by
  * the reference), where exact blocks take S = s_q s_k (Q8 . K8) on the INT8
  * matrix cores, Q8 = the query row at one scale s_q = max|q| / 127; routing,
- * centroid terms and P V stay BF16 (forms 0-2 only).
+ * centroid terms and P V stay BF16; sol_quantize_keys's rows_mode must be
+ * nonzero exactly when tiles is NULL here.
  * workgroup_form: 0 picks the schedule by launch size (1 below 512 query-block
  * pairs, else 2); 1 or 2 force one or two query blocks per 4-wave workgroup
- * (bit-identical results), 3 the 8-wave ping-pong workgroup (two query
- * blocks: their common exact blocks streamed once, the rest in pairs; equal
- * to the other forms within FP32 summation order; an experimental schedule,
- * slower than form 2 on MI355X).  No counterpart in the reference (one
- * Triton program per query block). */
+ * (bit-identical results).  No counterpart in the reference (one Triton
+ * program per query block).
+ * Key blocks: with tiles NULL ("rows mode") the kernels DMA each key block's
+ * rows straight from k / v (strides {batch, token, head} as in sol_pool_kv;
+ * requires key_index-free, equal-length keys: key_lengths NULL, key_tokens >=
+ * 64, token strides below 2^24 elements); otherwise from the tile pairs
+ * sol_pool_kv wrote, and k / v are ignored (may be NULL). */
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t sequence_length, int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,
+                      const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                       const void* tiles, const void* ctiles,
                       const float* key_mean, const float* key_var, const float* key_cov,
                       const uint8_t* protection, const int32_t* pair_strides,
@@ -177,14 +184,21 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       int workgroup_form, void* stream);
 
 /* INT8 K tiles for the quantised-QK experiment of sol_attention_fwd: per key
- * block of the tile pairs that sol_pool_kv wrote (tiles, as in
- * sol_pool_sizes), one scale s_k = max|K| / 127 over the block (k8_scales,
- * fp32 [batch, heads, NKB]) and K8 = rint(K * 127 / max|K|) clamped to +-127
- * (k8_tiles, int8 [batch, heads, NKB, 64 * head_dim]; 16-byte chunk c of row r
- * at chunk c ^ ((r >> 1) & 7) for head_dim 128, c ^ ((r >> 2) & 3) for 64).
- * No counterpart in the reference (ROADMAP.md:14-16 asks for the experiment). */
-int sol_quantize_keys(const void* tiles, int64_t batch, int64_t key_tokens, int64_t heads,
-                      int64_t head_dim, void* k8_tiles, float* k8_scales, void* stream);
+ * block of K (k, k_strides, key_index, key_lengths, sequence_length as in
+ * sol_pool_kv), one scale s_k = max|K| / 127 over the block's keys
+ * (k8_scales, fp32 [batch, heads, NKB]) and K8 = rint(K * 127 / max|K|)
+ * clamped to +-127 (k8_tiles, int8 [batch, heads, NKB, 64 * head_dim];
+ * 16-byte chunk c of row r at chunk c ^ ((r >> 1) & 7) for head_dim 128,
+ * c ^ ((r >> 2) & 3) for 64).  Row r of block j's tile is key 64 j + r (zero
+ * past the end), except with rows_mode (for a rows-mode sol_attention_fwd
+ * call, whose partial last block holds the sequence's last 64 keys): there
+ * the partial last block's tile holds keys key_tokens - 64 + r, quantised
+ * with the block's own scale.  No counterpart in the reference
+ * (ROADMAP.md:14-16 asks for the experiment). */
+int sol_quantize_keys(const void* k, const int64_t* k_strides, const int64_t* key_index,
+                      const int32_t* key_lengths, int64_t sequence_length, int64_t batch,
+                      int64_t key_tokens, int64_t heads, int64_t head_dim, int rows_mode,
+                      void* k8_tiles, float* k8_scales, void* stream);
 
 /* Packed-block protection of indexed windows, built on the GPU: the
  * protection part of `IndexedPlan.create` (indexed.py:27-62).  Block (w, qb,
@@ -205,7 +219,9 @@ int sol_plan_protection(const int64_t* rows, const int64_t* keys, const int32_t*
 
 /* Non-causal BF16 attention over all keys, FP32 softmax and accumulation.
  * Replaces `launch_dense` (kernels.py:193-200; kernel kernels.py:67-98).
- * tiles: workspace of sol_pool_sizes()[1] bytes (filled here).
+ * tiles: NULL when the keys qualify for rows mode (key_tokens >= 64, token
+ * strides below 2^24 elements; see sol_attention_fwd), else a workspace of
+ * sol_pool_sizes()[1] bytes (filled here).
  * out: contiguous BF16 [batch, query_tokens, heads, head_dim]. */
 int sol_dense_fwd(const void* q, const int64_t* q_strides,
                   const void* k, const int64_t* k_strides,
@@ -223,13 +239,15 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides,
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * allocation).  The caller passes Q/K/V, out (contiguous BF16 [batch,
  * query_tokens, heads, head_dim]) and counts (NULL or int32 [batch, NQB,
- * heads]); arguments as in sol_attention_fwd.  The pooled keys take about
- * 2 * head_dim * 2 bytes per key token and head (the K / V^T tiles) plus the
- * centroids: problems needing more than SOL_NOALLOC_SCRATCH_BYTES (128 MiB:
- * batch * heads * key_tokens up to about 250,000 at head_dim 128, 500,000 at
- * 64) return SOL_ERR_UNSUPPORTED before any GPU work.  Every call on one GPU shares that GPU's array: calls that
- * overlap on one GPU (different streams or threads) race and must be
- * serialised by the caller. */
+ * heads]); arguments as in sol_attention_fwd.  The pooled keys are the
+ * centroid tiles, head_dim / 16 bytes per key token and head (padded to
+ * whole 64-block tiles), and the moments; key blocks are read straight from K
+ * and V (rows mode), except for fewer than 64 keys or token strides of 2^24
+ * elements or more, where the block tiles (4 * head_dim bytes per key token
+ * and head) join them.  Problems needing more than SOL_NOALLOC_SCRATCH_BYTES
+ * (128 MiB) return SOL_ERR_UNSUPPORTED before any GPU work.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (different
+ * streams or threads) race and must be serialised by the caller. */
 int sol_attention_noalloc(const void* q, const int64_t* q_strides,
                           const void* k, const int64_t* k_strides,
                           const void* v, const int64_t* v_strides,

@@ -16,7 +16,7 @@ import os
 import torch
 
 BLOCK = 64
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -37,6 +37,7 @@ _SIGNATURES = {
     "sol_pair_workspace_size": ([_i64, _i64, _i64, _i64], ctypes.c_int64),
     "sol_pair_strides": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64,
+                           _p, _i64p, _p, _i64p,
                            _p, _p, _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
                            _p, _p, _p, _p, _p, _p, _p, _p, _int, _p], ctypes.c_int),
@@ -45,7 +46,7 @@ _SIGNATURES = {
     "sol_plan_protection": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
     "sol_key_covariance_workspace_size": ([_i64, _i64, _i64], ctypes.c_int64),
     "sol_key_covariance": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
-    "sol_quantize_keys": ([_p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "sol_quantize_keys": ([_p, _i64p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _p, _p, _p], ctypes.c_int),
     "sol_attention_noalloc": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
                                _dbl, _dbl, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
 }
@@ -110,6 +111,15 @@ def _tiles(b, h, nkb, d, device):
     return torch.empty((b, h, nkb, 2, BLOCK * d), device=device, dtype=torch.bfloat16)
 
 
+def rows_mode(k, v, key_index=None, key_lengths=None):
+    """Whether the attention kernels read key blocks straight from K / V rows
+    (no pooled block tiles): plain strided keys of equal length, at least one
+    block of them, token strides below 2^24 elements (``include/sol_attn_amd.h``)."""
+    tk = k.shape[1]
+    return (key_index is None and key_lengths is None and tk >= BLOCK
+            and k.stride(1) < (1 << 24) and v.stride(1) < (1 << 24))
+
+
 _ALIGN = 256  # byte alignment of each buffer carved from a workspace
 
 
@@ -137,8 +147,11 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None, stream=None, v
     the buffers' device addresses (``*_ptr``) and, with ``views``, tensor views
     ``ctiles`` ``[B, H, NCT, 2, 64 D]`` (block centroids), ``tiles``
     ``[B, H, NKB, 2, 64 D]`` and ``mean``/``var`` ``[B, H, D]`` (None without
-    ``moments``); layouts per ``include/sol_attn_amd.h``.  ``qk_int8`` also
-    quantises the K tiles (``sol_quantize_keys``) for the INT8-QK experiment.
+    ``moments``); layouts per ``include/sol_attn_amd.h``.  The block tiles
+    exist only when the keys do not qualify for rows mode (:func:`rows_mode`);
+    otherwise the attention kernels read K and V themselves, which the dict
+    keeps (``k``, ``v``).  ``qk_int8`` also quantises K per block
+    (``sol_quantize_keys``) for the INT8-QK experiment.
     """
     lib = library()
     indexed = key_index is not None
@@ -148,36 +161,39 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None, stream=None, v
     else:
         b, tk, h, d = k.shape
     k, v = _rows(k), _rows(v)
+    rows = not indexed and rows_mode(k, v, None, key_lengths)
     nkb = -(-tk // BLOCK)
     nct = -(-nkb // BLOCK)
     dev = k.device
     if stream is None:
         stream = _stream(dev)
     tile = 2 * BLOCK * d * 2  # bytes of one K/V tile pair
-    sizes = [b * h * nct * tile, b * h * nkb * tile]
+    sizes = [b * h * nct * tile, 0 if rows else b * h * nkb * tile]
     sizes += [b * h * -(-nkb // 16) * 2 * d * 4, b * h * d * 4, b * h * d * 4] if moments else [0, 0, 0]
     if qk_int8:
         sizes += [b * h * nkb * BLOCK * d, b * h * nkb * 4]
     offsets, total = _carve(sizes)
     ws = torch.empty(total, device=dev, dtype=torch.uint8)
     base = ws.data_ptr()
-    ctiles, tiles = base + offsets[0], base + offsets[1]
+    ctiles, tiles = base + offsets[0], None if rows else base + offsets[1]
     sums, mean, var = (base + o for o in offsets[2:5]) if moments else (None, None, None)
     _check(lib.sol_pool_kv(k.data_ptr(), _strides(k, indexed), v.data_ptr(), _strides(v, indexed),
                            _ptr(key_index), _ptr(key_lengths), k.shape[0] if indexed else 0,
                            b, tk, h, d, ctiles, tiles, sums, mean, var, stream))
     pooled = {"workspace": ws, "shape": (b, h, d), "ctiles_ptr": ctiles, "tiles_ptr": tiles,
               "mean_ptr": mean, "var_ptr": var, "cov_ptr": None, "key_tokens": tk,
-              "key_blocks": nkb, "key_lengths": key_lengths, "k8_ptr": None, "k8_scale_ptr": None}
+              "key_blocks": nkb, "key_lengths": key_lengths, "k8_ptr": None, "k8_scale_ptr": None,
+              "k": k if rows else None, "v": v if rows else None}
     if qk_int8:
         k8, k8s = base + offsets[5], base + offsets[6]
-        _check(lib.sol_quantize_keys(tiles, b, tk, h, d, k8, k8s, stream))
+        _check(lib.sol_quantize_keys(k.data_ptr(), _strides(k, indexed), _ptr(key_index), _ptr(key_lengths),
+                                     k.shape[0] if indexed else 0, b, tk, h, d, int(rows), k8, k8s, stream))
         pooled["k8_ptr"], pooled["k8_scale_ptr"] = k8, k8s
         if views:
             pooled["k8_scale"] = _region(ws, offsets[6], torch.float32, (b, h, nkb))
     if views:
         pooled["ctiles"] = _region(ws, offsets[0], torch.bfloat16, (b, h, nct, 2, BLOCK * d))
-        pooled["tiles"] = _region(ws, offsets[1], torch.bfloat16, (b, h, nkb, 2, BLOCK * d))
+        pooled["tiles"] = None if rows else _region(ws, offsets[1], torch.bfloat16, (b, h, nkb, 2, BLOCK * d))
         pooled["mean"] = _region(ws, offsets[3], torch.float32, (b, h, d)) if moments else None
         pooled["var"] = _region(ws, offsets[4], torch.float32, (b, h, d)) if moments else None
     return pooled
@@ -283,9 +299,11 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     if protection is not None:
         prot = protection.contiguous().view(torch.uint8)
     strides = pair_strides(q, rows, stream=stream) if PAIRING else None
+    kr, vr = pooled["k"], pooled["v"]
     _check(lib.sol_attention_fwd(
         q.data_ptr(), _strides(q, indexed), _ptr(rows), q.shape[0] if indexed else 0,
         b, nq, nk, _ptr(pooled["key_lengths"]), h, d,
+        _ptr(kr), None if kr is None else _strides(kr), _ptr(vr), None if vr is None else _strides(vr),
         pooled["tiles_ptr"], pooled["ctiles_ptr"], pooled["mean_ptr"], pooled["var_ptr"], pooled["cov_ptr"],
         _ptr(prot), _ptr(strides), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
         out.data_ptr(), _ptr(rows if scatter else None), _ptr(counts),
@@ -351,8 +369,8 @@ def launch_dense(q, k, v, scale):
     b, nq, h, d = q.shape
     nk = k.shape[1]
     out = torch.empty((b, nq, h, d), device=q.device, dtype=torch.bfloat16)
-    tiles = _tiles(b, h, -(-nk // BLOCK), d, q.device)
+    tiles = None if rows_mode(k, v) else _tiles(b, h, -(-nk // BLOCK), d, q.device)
     _check(lib.sol_dense_fwd(q.data_ptr(), _strides(q), k.data_ptr(), _strides(k), v.data_ptr(), _strides(v),
-                             b, nq, nk, h, d, float(scale), tiles.data_ptr(), out.data_ptr(),
+                             b, nq, nk, h, d, float(scale), _ptr(tiles), out.data_ptr(),
                              _stream(q.device)))
     return out

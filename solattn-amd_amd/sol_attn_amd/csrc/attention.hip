@@ -52,6 +52,7 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
   constexpr int KT = Shape<D>::KT, DT = Shape<D>::DT;
   static_assert(KT == 2 * DT, "score and P V chunk counts match");
   const FragLane<D> fl(fresh(col), fresh(hh));
+  const uint32_t vbase = fl.v_base(buf);
   u32x4 k0[KT], k1[KT];
 #pragma unroll
   for (int ks = 0; ks < KT; ++ks) k0[ks] = fl.k(buf, 0, ks);
@@ -74,7 +75,7 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
     if (ks >= KT / 2) {  // two of half 0's 2 DT = KT V^T fragments per chunk
 #pragma unroll
       for (int f = 2 * (ks - KT / 2); f < 2 * (ks - KT / 2) + 2; ++f)
-        va[f / DT][f % DT] = fl.v(buf, 0, f / DT, f % DT);
+        va[f / DT][f % DT] = fl.v(vbase, 0, f / DT, f % DT);
     }
     refill.template after_step<2 * KT>(KT + ks);
     chunk_end();
@@ -85,7 +86,7 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
   for (int f = 0; f < 2 * DT; ++f) {
     const int c4 = f / DT, dt = f % DT;
     st.acc[dt] = mfma32x32x16(as_bf16x8(va[c4][dt]), h0.pb(c4), st.acc[dt]);
-    vb[c4][dt] = fl.v(buf, 1, c4, dt);
+    vb[c4][dt] = fl.v(vbase, 1, c4, dt);
     h1.template part<2 * DT>(f, st, c);
     chunk_end();
   }
@@ -109,22 +110,36 @@ __device__ __forceinline__ void full_tile(State<D>& st, const uint16_t* buf,
   tile_attend<D, false>(st, buf, qf, col, hh, c, NoBias{}, refill);
 }
 
-// Exact block j: a full block, or the tail block whose keys at or past tk
-// start at -inf.  Only a stream's last exact tile can be the tail block.
-template <int D, typename Refill>
+// The rows of the sequence's partial last block j that hold its tk - 64 j
+// keys: [64 - len, 64) when the block was DMA'd from rows shifted back to the
+// sequence's last 64 rows (SHIFTED), else [0, len) (zero-padded tiles).
+// Returned relative to this lane's rows, as the bounds a <= tile_row(t, e, 0)
+// < z of the present keys.
+template <bool SHIFTED>
+__device__ __forceinline__ int2 tail_rows(int j, int tk, int hh) {
+  const int len = tk - j * kBlock;
+  const int lo = SHIFTED ? kBlock - len : 0;
+  return make_int2(fresh(lo - 4 * hh), fresh(lo + len - 4 * hh));
+}
+
+// Exact block j: a full block, or the partial last block, whose absent keys
+// start at -inf.  Only a stream's last exact tile can be that block.
+template <int D, bool SHIFTED, typename Refill>
 __device__ __forceinline__ void exact_tile(State<D>& st, const uint16_t* buf, int j, int tk,
                                            const bf16x8 (&qf)[Shape<D>::KT], int col, int hh, float c,
                                            const Refill& refill) {
   if ((j + 1) * kBlock <= tk) {
     full_tile<D>(st, buf, qf, col, hh, c, refill);
   } else {
-    const int lane_keys = fresh(tk - j * kBlock - 4 * hh);  // keys from this lane's first row on
+    const int2 present = tail_rows<SHIFTED>(j, tk, hh);
     tile_attend<D, true>(st, buf, qf, col, hh, c,
                          [&](int t) {
                            f32x16 bias;
 #pragma unroll
-                           for (int e = 0; e < 16; ++e)
-                             bias[e] = tile_row(t, e, 0) < lane_keys ? 0.f : kNegInf;
+                           for (int e = 0; e < 16; ++e) {
+                             const int row = tile_row(t, e, 0);
+                             bias[e] = row >= present.x && row < present.y ? 0.f : kNegInf;
+                           }
                            return bias;
                          },
                          refill);
@@ -179,10 +194,11 @@ __device__ __forceinline__ void centroid_tile(State<D>& st, const uint16_t* buf,
 // 2 D / 32 score chunks.
 template <int D, bool TAIL, typename Refill>
 __device__ __forceinline__ void tile_attend_i8(State<D>& st, const uint16_t* buf, const i32x4 (&q8)[D / 32],
-                                               int col, int hh, float c8, int lane_keys, const Refill& refill) {
+                                               int col, int hh, float c8, int2 present, const Refill& refill) {
   constexpr int K8 = D / 32, DT = Shape<D>::DT;
   static_assert(K8 == DT, "two V^T fragments of half 0 per score chunk");
   const FragLane<D> fl(fresh(col), fresh(hh));
+  const uint32_t vbase = fl.v_base(buf);
   const int8_t* kbuf = reinterpret_cast<const int8_t*>(buf);
   const int c0 = fresh(col);
   const int krow = c0 * D;                                 // row col of the K8 tile
@@ -195,7 +211,7 @@ __device__ __forceinline__ void tile_attend_i8(State<D>& st, const uint16_t* buf
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       sc[e] = float(x[e]);
-      if (TAIL && tile_row(t, e, 0) >= lane_keys) sc[e] = kNegInf;
+      if (TAIL && (tile_row(t, e, 0) < present.x || tile_row(t, e, 0) >= present.y)) sc[e] = kNegInf;
     }
     return sc;
   };
@@ -221,7 +237,7 @@ __device__ __forceinline__ void tile_attend_i8(State<D>& st, const uint16_t* buf
     if (ks == 0) h0.s = to_scores(i0, 0);
     h0.template part<K8>(ks, st, c8);
 #pragma unroll
-    for (int f = 2 * ks; f < 2 * ks + 2; ++f) va[f / DT][f % DT] = fl.v(buf, 0, f / DT, f % DT);
+    for (int f = 2 * ks; f < 2 * ks + 2; ++f) va[f / DT][f % DT] = fl.v(vbase, 0, f / DT, f % DT);
     refill.template after_step<2 * K8>(K8 + ks);
     chunk_end();
   }
@@ -231,7 +247,7 @@ __device__ __forceinline__ void tile_attend_i8(State<D>& st, const uint16_t* buf
   for (int f = 0; f < 2 * DT; ++f) {
     const int c4 = f / DT, dt = f % DT;
     st.acc[dt] = mfma32x32x16(as_bf16x8(va[c4][dt]), h0.pb(c4), st.acc[dt]);
-    vb[c4][dt] = fl.v(buf, 1, c4, dt);
+    vb[c4][dt] = fl.v(vbase, 1, c4, dt);
     if (f == 0) h1.s = to_scores(i1, 1);
     h1.template part<2 * DT>(f, st, c8);
     chunk_end();
@@ -294,6 +310,20 @@ __device__ __forceinline__ TileRuns<Sel, Hit, Miss> tile_runs(Sel selected, Hit 
 template <int D, int NT, typename Source>
 __device__ __forceinline__ auto bf16_refills(Source source, int wave, int lane) {
   return [=](int ref, uint32_t lds) { return TileRefill<D, NT>(source(ref), lds, wave, lane); };
+}
+
+// Refill factory of key block j's K + V tile pair for (entry b, head h):
+// from the pooled tile pairs (KT: indexed windows, or fewer than 64 keys) or
+// straight from the K / V rows.
+template <int D, int NT, bool KT>
+__device__ __forceinline__ auto kv_refills(const AttnParams& p, int b, int h, int wave, int lane) {
+  if constexpr (KT) {
+    const uint16_t* tiles = p.tiles + (int64_t(b) * p.H + h) * p.NKB * Shape<D>::TILE;
+    return bf16_refills<D, NT>([=](int j) { return tiles + int64_t(j) * Shape<D>::TILE; }, wave, lane);
+  } else {
+    const KvRows<D, NT> rows = kv_rows<D, NT>(p, b, h, wave * kWave + lane);
+    return [=](int j, uint32_t lds) { return RowRefill<D, NT>(rows, j, lds, wave); };
+  }
 }
 
 template <int D, int NT, int R, typename Next, typename Make, typename Runs, typename Last>
@@ -421,14 +451,14 @@ struct RangeCursor {
 // The bound names 256 threads for both workgroup forms, so the one-block form
 // (128 threads) is held to the same budget (with its own 128-thread bound the
 // compiler moves values through AGPRs instead).
-template <int D, int G, int R, bool Q8>
+template <int D, int G, int R, bool Q8, bool KT>
 __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   using S = Shape<D>;
   using TL = TileLayout<D>;
   constexpr int NT = 128 * G;
   constexpr int kMaskWords = kMaxKeyBlocks / 32;
   static_assert(R * S::TILE >= G * kBlock * S::KS, "Q staging must fit in the ring");
-  __shared__ __align__(16) uint16_t ring[R * S::TILE];  // Q staging, then the tile ring
+  __shared__ __align__(256) uint16_t ring[R * S::TILE];  // Q staging, then the tile ring
   __shared__ float s_qm[G][D];
   __shared__ float s_red[G][4];
   __shared__ float s_cut[G];
@@ -637,7 +667,7 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   // Tile ids travel as tags 2 j + own-selection bit (UnionCursor).
   UnionCursor<G> cursor{&s_mask[0][0], s_mask[qg], kMaskWords, nkb};
   const int count = cursor.count();
-  const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
+  const auto kv = kv_refills<D, NT, KT>(p, b, h, wave, lane);
   auto selected = [](int tag) { return (tag & 1) != 0; };
   auto miss = [&](const uint16_t*, int, const auto& refill) { refill.all(); };
   if constexpr (!Q8) {
@@ -645,29 +675,28 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
       full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
     };
     tile_stream<D, NT, R>(
-        ring, count, cursor, bf16_refills<D, NT>([=](int tag) { return tiles + int64_t(tag >> 1) * S::TILE; },
-                                                 wave, lane),
+        ring, count, cursor, [=](int tag, uint32_t lds) { return kv(tag >> 1, lds); },
         tile_runs(selected, hit, miss),
         [&](const uint16_t* buf, int tag, const auto& refill) {
           if (tag & 1) {
-            exact_tile<D>(st, buf, tag >> 1, tk, qf, col, hh, scale_log2, refill);
+            exact_tile<D, !KT>(st, buf, tag >> 1, tk, qf, col, hh, scale_log2, refill);
           } else {
             refill.all();
           }
         },
         wave, lane);
   } else {
-    // Quantised QK: INT8 K tiles and their scales (the V^T halves still come
-    // from the BF16 tile pairs).
+    // Quantised QK: INT8 K tiles and their scales (the V tiles as in the
+    // BF16 stream).
     const int8_t* k8 = p.k8 + head * p.NKB * K8Layout<D>::kBytes;
     const float* k8s = p.k8_scale + head * p.NKB;
     auto make = [=](int tag, uint32_t lds) {
-      const int64_t j = tag >> 1;
-      return Q8Refill<D, NT>(k8 + j * K8Layout<D>::kBytes, tiles + j * S::TILE + TileLayout<D>::kElems, lds,
-                             wave, lane);
+      const int j = tag >> 1;
+      return Q8Refill<D, NT, decltype(kv(0, 0u))>(k8 + int64_t(j) * K8Layout<D>::kBytes, lds, wave, lane,
+                                                  kv(j, lds));
     };
     auto hit = [&](const uint16_t* buf, int tag, const auto& refill) {
-      tile_attend_i8<D, false>(st, buf, q8, col, hh, csq * k8s[tag >> 1], 0, refill);
+      tile_attend_i8<D, false>(st, buf, q8, col, hh, csq * k8s[tag >> 1], int2{}, refill);
     };
     tile_stream<D, NT, R>(
         ring, count, cursor, make, tile_runs(selected, hit, miss),
@@ -676,9 +705,9 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
             const int j = tag >> 1;
             const float c8 = csq * k8s[j];
             if ((j + 1) * kBlock <= tk)
-              tile_attend_i8<D, false>(st, buf, q8, col, hh, c8, 0, refill);
+              tile_attend_i8<D, false>(st, buf, q8, col, hh, c8, int2{}, refill);
             else
-              tile_attend_i8<D, true>(st, buf, q8, col, hh, c8, fresh(tk - j * kBlock - 4 * hh), refill);
+              tile_attend_i8<D, true>(st, buf, q8, col, hh, c8, tail_rows<!KT>(j, tk, hh), refill);
           } else {
             refill.all();
           }
@@ -690,14 +719,14 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   if (live) store_output<D>(p, b, h, qb * kBlock + myq, hh, st);
 }
 
-template <int D>
+template <int D, bool KT>
 __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   using S = Shape<D>;
   constexpr int NT = 256;
   constexpr int QROWS = 128;
   constexpr int Q_ELEMS = QROWS * S::KS;
   constexpr int RING = 2 * S::TILE > Q_ELEMS ? 2 * S::TILE : Q_ELEMS;
-  __shared__ __align__(16) uint16_t ring[RING];
+  __shared__ __align__(256) uint16_t ring[RING];
 
   const int nq_tiles = (p.Tq + QROWS - 1) / QROWS;
   const TileTask task = xcd_task(blockIdx.x, nq_tiles);
@@ -729,16 +758,14 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   state_init(st);
   const int tk = p.Tk;
   const float scale_log2 = p.scale_log2;
-  const uint16_t* tiles = p.tiles + head * p.NKB * S::TILE;
   auto always = [](int) { return true; };
   auto hit = [&](const uint16_t* buf, int, const auto& refill) {
     full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
   };
   tile_stream<D, NT, 2>(
-      ring, p.NKB, RangeCursor{0}, bf16_refills<D, NT>([=](int j) { return tiles + int64_t(j) * S::TILE; }, wave, lane),
-      tile_runs(always, hit, hit),
+      ring, p.NKB, RangeCursor{0}, kv_refills<D, NT, KT>(p, b, h, wave, lane), tile_runs(always, hit, hit),
       [&](const uint16_t* buf, int j, const auto& refill) {
-        exact_tile<D>(st, buf, j, tk, qf, col, hh, scale_log2, refill);
+        exact_tile<D, !KT>(st, buf, j, tk, qf, col, hh, scale_log2, refill);
       },
       wave, lane);
   store_output<D>(p, b, h, q0 + myq, hh, st);
@@ -751,7 +778,7 @@ constexpr int kSolRing = 2;
 // which doubles the workgroups and has no union to stream.  Both forms give
 // bit-identical results (a wave's tiles, their order and its softmax state
 // do not depend on its partner).  AttnParams::workgroup_form 1 or 2 forces
-// one form (tests run both); 3 runs the ping-pong kernel (attention_pp.hip).
+// one form (tests run both).
 constexpr int64_t kSmallLaunchGroups = 512;
 
 template <int D, int G>
@@ -759,16 +786,23 @@ void launch_sol_group(const AttnParams& p, hipStream_t stream) {
   // Grid of sol_task: the sink-holding tiles of every head, then xcd_task's.
   const int ntiles = (p.NQB + G - 1) / G, front = std::min(p.q_sink_blocks, ntiles);
   const unsigned grid = unsigned(front) * unsigned(p.B * p.H) + xcd_grid(p.B * p.H, ntiles - front);
-  if (p.k8)
-    hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, true>), dim3(grid), dim3(128 * G), 0, stream, p);
-  else
-    hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, false>), dim3(grid), dim3(128 * G), 0, stream, p);
+  // Key blocks from pooled tile pairs (p.tiles) or straight from K / V rows.
+  if (p.tiles) {
+    if (p.k8)
+      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, true, true>), dim3(grid), dim3(128 * G), 0, stream, p);
+    else
+      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, false, true>), dim3(grid), dim3(128 * G), 0, stream, p);
+  } else {
+    if (p.k8)
+      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, true, false>), dim3(grid), dim3(128 * G), 0, stream, p);
+    else
+      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, false, false>), dim3(grid), dim3(128 * G), 0, stream, p);
+  }
 }
 
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
   int g = int64_t(p.B) * p.H * ((p.NQB + 1) / 2) < kSmallLaunchGroups ? 1 : 2;
-  if (p.workgroup_form >= 1 && p.workgroup_form <= 3) g = p.workgroup_form;
-  if (g == 3) return launch_sol_pp(p, D, stream);
+  if (p.workgroup_form == 1 || p.workgroup_form == 2) g = p.workgroup_form;
   if (D == 128) {
     if (g == 1) launch_sol_group<128, 1>(p, stream); else launch_sol_group<128, 2>(p, stream);
   } else {
@@ -778,12 +812,18 @@ hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
 }
 
 hipError_t launch_dense(const AttnParams& p, int D, hipStream_t stream) {
-  if (p.workgroup_form == 3) return launch_dense_pp(p, D, stream);
   const unsigned grid = xcd_grid(p.B * p.H, (p.Tq + 127) / 128);
-  if (D == 128)
-    hipLaunchKernelGGL(dense_attention_kernel<128>, dim3(grid), dim3(256), 0, stream, p);
-  else
-    hipLaunchKernelGGL(dense_attention_kernel<64>, dim3(grid), dim3(256), 0, stream, p);
+  if (D == 128) {
+    if (p.tiles)
+      hipLaunchKernelGGL((dense_attention_kernel<128, true>), dim3(grid), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((dense_attention_kernel<128, false>), dim3(grid), dim3(256), 0, stream, p);
+  } else {
+    if (p.tiles)
+      hipLaunchKernelGGL((dense_attention_kernel<64, true>), dim3(grid), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL((dense_attention_kernel<64, false>), dim3(grid), dim3(256), 0, stream, p);
+  }
   return hipGetLastError();
 }
 

@@ -1,5 +1,4 @@
-// Device building blocks shared by the SOL attention kernels (attention.hip,
-// attention_pp.hip): the workgroup -> query-tile maps, the FP32 online-softmax
+// Device building blocks of the SOL attention kernels (attention.hip): the workgroup -> query-tile maps, the FP32 online-softmax
 // state of a wave, the LDS DMA tile refill, the MFMA operand reads from the
 // swizzled tiles, and the output store.
 #pragma once
@@ -59,7 +58,7 @@ struct Shape {
   static constexpr int DC = D / 8;   // 16-byte chunks per row
   static constexpr int KT = D / 16;  // MFMA k-steps over the head dimension
   static constexpr int DT = D / 32;  // 32-row output tiles over the head dimension
-  static constexpr int TILE = 2 * kBlock * D;  // K + V^T tile elements per 64-wide tile
+  static constexpr int TILE = 2 * kBlock * D;  // K + V tile elements per 64-key tile
 };
 
 // One wave's FP32 online-softmax state for its 32 queries (one per lane pair).
@@ -174,37 +173,123 @@ struct TileRefill {
   }
 };
 
-// DMA of the quantised-QK experiment's tiles into one LDS slot: the INT8 K
-// tile of a key block (64 rows x D bytes, from the INT8 tile array) at the
-// slot's start, then the V^T half of its BF16 tile pair at the V^T offset
-// of the BF16 layout (so the P V operand reads are unchanged).  Rounds as in
-// TileRefill: the K8 rounds first, then the V^T rounds.
+// Key blocks DMA'd into an LDS slot as a K + V tile pair (TileLayout)
+// straight from the caller's K and V rows ("rows mode"; the other source is
+// a pooled tile pair array, TileRefill).  Each round moves RPR = NT 16 / (2 D)
+// key rows of K (or V): wave w's 1 KB piece of the slot, lane l's 16 bytes at
+// LDS byte 16 (r NT + 64 w + l), is the chunk that position holds in the
+// tile layout, so lane l reads row r RPR + (its round-0 row), chunk (its
+// chunk).  The per-lane byte offsets klane / vlane (row * row stride +
+// 16 chunk) are the same in every round, except for the K swizzle of
+// D = 128 with 128 threads, whose rounds alternate klane / klane_odd.  The
+// sequence's partial last block is read shifted back to rows Tk - 64 ..
+// Tk - 1 (all present; Tk >= 64 in rows mode), so its keys sit in the
+// tile's last Tk - 64 (NKB - 1) rows and the rows before them, keys of the
+// previous block, are masked out by the consumer.
 template <int D, int NT>
+struct KvRows {
+  static constexpr int kHalfRounds = kBlock * D * 2 / 16 / NT;  // DMA rounds per K (or V) tile
+  static constexpr int kRowsPerRound = NT * 16 / (2 * D);
+  static constexpr bool kOddK = D == 128 && NT == 128;          // K swizzle period of two rounds
+  uint64_t k, v;            // byte address of key row 0 of this (entry, head)
+  uint64_t stk, stv;        // bytes between key rows
+  int last, last_row;       // the partial last block (-1: none) and its first row
+  uint32_t klane, vlane, klane_odd;  // klane_odd: kOddK only
+};
+
+template <int D, int NT>
+__device__ __forceinline__ KvRows<D, NT> kv_rows(const AttnParams& p, int b, int h, int tid) {
+  using TL = TileLayout<D>;
+  using Src = KvRows<D, NT>;
+  Src s;
+  s.stk = uint64_t(p.k.st) * 2;
+  s.stv = uint64_t(p.v.st) * 2;
+  s.k = uniform64(reinterpret_cast<uint64_t>(p.k.base + int64_t(b) * p.k.sb + int64_t(h) * p.k.sh));
+  s.v = uniform64(reinterpret_cast<uint64_t>(p.v.base + int64_t(b) * p.v.sb + int64_t(h) * p.v.sh));
+  s.last = p.Tk % kBlock ? p.Tk / kBlock : -1;
+  s.last_row = p.Tk - kBlock;
+  const int w = tid >> 6, l = tid & 63;
+  // K, row-major: the wave's 1 KB piece holds 512 / D rows.
+  const int krow = w * (512 / D) + l / (D / 8), kpc = l % (D / 8);
+  s.klane = uint32_t(krow * int64_t(s.stk) + 16 * (kpc ^ TL::k_swizzle(krow)));
+  s.klane_odd = Src::kOddK ? uint32_t(krow * int64_t(s.stk) + 16 * (kpc ^ TL::k_swizzle(krow + Src::kRowsPerRound)))
+                           : s.klane;
+  // V, row quads of 8 D bytes: position 16 m of quad q holds row
+  // 4 q + ((m >> 2) & 3), chunk 4 (m >> 4) + (m & 3).
+  const int pos = w * 1024 + 16 * l;
+  const int q = pos / (8 * D), m = (pos % (8 * D)) / 16;
+  s.vlane = uint32_t((4 * q + ((m >> 2) & 3)) * int64_t(s.stv) + 16 * (4 * (m >> 4) + (m & 3)));
+  return s;
+}
+
+// DMA of key block j from rows into the LDS slot at dst_lds (wave w's piece
+// of round r at dst_lds + 1024 w + 16 r NT): the K rounds, then the V
+// rounds; issued whole or a few rounds at a time, as TileRefill.
+template <int D, int NT>
+struct RowRefill {
+  using Src = KvRows<D, NT>;
+  static constexpr int kHalf = Src::kHalfRounds;
+  static constexpr int kRounds = 2 * kHalf;
+  uint64_t ksrc, vsrc, kstep, vstep;
+  uint32_t klane, vlane, klane_odd;
+  uint32_t lds;
+
+  __device__ __forceinline__ RowRefill(const Src& src, int j, uint32_t dst_lds, int wave)
+      : klane(src.klane), vlane(src.vlane), klane_odd(src.klane_odd) {
+    const int64_t row = j == src.last ? src.last_row : int64_t(j) * kBlock;
+    ksrc = uniform64(src.k + uint64_t(row) * src.stk);
+    vsrc = uniform64(src.v + uint64_t(row) * src.stv);
+    kstep = Src::kRowsPerRound * src.stk;
+    vstep = Src::kRowsPerRound * src.stv;
+    lds = uint32_t(__builtin_amdgcn_readfirstlane(dst_lds + uint32_t(wave) * (kWave * 16)));
+  }
+  __device__ __forceinline__ void round(int r) const {
+    if (r < kHalf) {
+      const uint32_t lane = (Src::kOddK && (r & 1)) ? klane_odd : klane;
+      dma16(ksrc + uint64_t(r) * kstep, lane, lds + uint32_t(r * NT * 16));
+    } else {
+      const int rv = r - kHalf;
+      dma16(vsrc + uint64_t(rv) * vstep, vlane, lds + uint32_t(TileLayout<D>::kElems * 2 + rv * NT * 16));
+    }
+  }
+  __device__ __forceinline__ void all() const {
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) round(r);
+  }
+  template <int N>
+  __device__ __forceinline__ void after_step(int k) const {
+#pragma unroll
+    for (int r = k * kRounds / N; r < (k + 1) * kRounds / N; ++r) round(r);
+  }
+};
+
+// DMA for the quantised-QK experiment's exact tiles: the INT8 K tile of a
+// key block (64 rows x D bytes, contiguous in the INT8 tile array) at the
+// slot's start, then the block's V tile as the BF16 refill V moves it (Kv: a
+// RowRefill, or a TileRefill of the block's tile pair).  Rounds: the K8
+// rounds, then the V rounds.
+template <int D, int NT, typename Kv>
 struct Q8Refill {
   static constexpr int kK8Rounds = kBlock * D / 16 / NT;
-  static constexpr int kVRounds = kBlock * D * 2 / 16 / NT;
+  static constexpr int kVRounds = Kv::kRounds / 2;
   static constexpr int kRounds = kK8Rounds + kVRounds;
   static_assert(kK8Rounds * NT * 16 == kBlock * D, "INT8 tile must split evenly over the workgroup");
-  uint64_t k8src, vsrc;
-  uint32_t lds;
-  uint32_t lane_bytes;
+  uint64_t k8src;
+  uint32_t k8lds, lane_bytes;
+  Kv kv;
 
-  __device__ __forceinline__ Q8Refill(const int8_t* k8tile, const uint16_t* vt, uint32_t dst_lds, int wave,
-                                      int lane)
+  __device__ __forceinline__ Q8Refill(const int8_t* k8tile, uint32_t dst_lds, int wave, int lane, const Kv& v)
       : k8src(uniform64(reinterpret_cast<uint64_t>(k8tile) + uint64_t(wave) * (kWave * 16))),
-        vsrc(uniform64(reinterpret_cast<uint64_t>(vt) + uint64_t(wave) * (kWave * 16))),
-        lds(uint32_t(__builtin_amdgcn_readfirstlane(dst_lds + uint32_t(wave) * (kWave * 16)))),
-        lane_bytes(uint32_t(lane) * 16u) {}
+        k8lds(uint32_t(__builtin_amdgcn_readfirstlane(dst_lds + uint32_t(wave) * (kWave * 16)))),
+        lane_bytes(uint32_t(lane) * 16u), kv(v) {}
 
   __device__ __forceinline__ void round(int r) const {
     if (r < kK8Rounds) {
       uint32_t off = uint32_t(r) * (NT * 16);
       asm volatile("" : "+s"(off));
-      dma16(k8src + off, lane_bytes, lds + off);
+      dma16(k8src + off, lane_bytes, k8lds + off);
     } else {
-      uint32_t off = uint32_t(r - kK8Rounds) * (NT * 16);
-      asm volatile("" : "+s"(off));
-      dma16(vsrc + off, lane_bytes, lds + uint32_t(TileLayout<D>::kElems * 2) + off);
+      kv.round(r - kK8Rounds + kVRounds);
     }
   }
   __device__ __forceinline__ void all() const {
@@ -335,23 +420,44 @@ struct HalfSoftmax {
   }
 };
 
-// This lane's element offsets of its MFMA operand reads inside a K + V^T
-// tile pair (see TileLayout): K fragment (t, ks) at k_row + 32 t D +
-// (k_x ^ 16 ks), V^T fragment (t, c4, dt) at kElems + v_row + 2048 dt +
-// (v_x ^ (32 t + 16 c4)); the per-read parts are immediates or one XOR-add.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// This lane's offsets of its MFMA operand reads inside a K + V tile pair
+// (TileLayout).  K fragment (t, ks): key row 32 t + col, features
+// 16 ks + 8 hh .. +7, at element k_row + 32 t D + (k_x ^ 16 ks).  V^T
+// fragment (t, c4, dt): feature 32 dt + col and the 8 keys
+// 32 t + 16 c4 + 4 hh + {0..3} and {8..11} (the k-slot order of the score
+// result that P^T keeps), as two ds_read_b64_tr_b16.  A transpose read
+// hands lane 4 a + e of each 16-lane group element e of the 8-byte reads of
+// lanes a, a + 4, a + 8, a + 12, so lane j of the group reads key row
+// k0 + (j >> 2), features 4 (j & 3) .. +3 of its 16-feature group: in the
+// row-quad V layout that is byte v_lane = 2 (kElems + 8 (hh 4 CPR +
+// 4 ((col >> 2) & 3) + 2 (col >> 4) + ((col & 3) >> 1)) + 4 (col & 1)) of
+// the tile, and read (t, c4, dt) adds the immediate 64 CPR (8 t + 4 c4) +
+// 256 dt bytes (quads of 64 CPR bytes; its second half two quads on).
 template <int D>
 struct FragLane {
-  int k_row, k_x, v_row, v_x;
+  static constexpr int CPR = TileLayout<D>::kRowChunks;
+  int k_row, k_x;
+  uint32_t v_lane;
   __device__ __forceinline__ FragLane(int col, int hh)
-      : k_row(col * D),
-        k_x(TileLayout<D>::k_lane_xor(col, hh)),
-        v_row(TileLayout<D>::kElems + col * kBlock),
-        v_x(TileLayout<D>::vt_lane_xor(col, hh)) {}
+      : k_row(col * D), k_x(TileLayout<D>::k_lane_xor(col, hh)), v_lane(v_lane_bytes(col, hh)) {}
+  __device__ static __forceinline__ uint32_t v_lane_bytes(int col, int hh) {
+    const int chunk = hh * 4 * CPR + 4 * ((col >> 2) & 3) + 2 * (col >> 4) + ((col & 3) >> 1);
+    return uint32_t(2 * (TileLayout<D>::kElems + 8 * chunk + 4 * (col & 1)));
+  }
   __device__ __forceinline__ u32x4 k(const uint16_t* buf, int t, int ks) const {
     return *reinterpret_cast<const u32x4*>(buf + k_row + 32 * t * D + (k_x ^ (16 * ks)));
   }
-  __device__ __forceinline__ u32x4 v(const uint16_t* buf, int t, int c4, int dt) const {
-    return *reinterpret_cast<const u32x4*>(buf + v_row + 32 * kBlock * dt + (v_x ^ (32 * t + 16 * c4)));
+  // LDS byte address of this lane's V reads in the tile at buf.
+  __device__ __forceinline__ uint32_t v_base(const uint16_t* buf) const { return lds_address(buf) + v_lane; }
+  __device__ __forceinline__ u32x4 v(uint32_t vbase, int t, int c4, int dt) const {
+    const uint32_t a = vbase + uint32_t(64 * CPR * (8 * t + 4 * c4) + 256 * dt);
+    const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SOL_LDS i16x4*)(uintptr_t)a);
+    const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((SOL_LDS i16x4*)(uintptr_t)(a + 128u * CPR));
+    const u32x2 x = __builtin_bit_cast(u32x2, lo), y = __builtin_bit_cast(u32x2, hi);
+    const u32x4 r = {x[0], x[1], y[0], y[1]};
+    return r;
   }
 };
 

@@ -86,6 +86,29 @@ int scratch_on_current_device(void** ptr) {
 
 int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
+// Attention kernels DMA key blocks straight from K / V rows ("rows mode",
+// no pooled tiles) when the keys are plain strided rows of equal length, at
+// least one block of them, with row strides whose 64-row spans fit the
+// kernels' 32-bit lane offsets.
+bool rows_mode_possible(const int64_t* key_index, const int32_t* key_lengths, int64_t key_tokens,
+                        const int64_t* k_strides, const int64_t* v_strides) {
+  return !key_index && !key_lengths && key_tokens >= SOL_BLOCK && k_strides && v_strides &&
+         k_strides[1] < (int64_t(1) << 24) && v_strides[1] < (int64_t(1) << 24);
+}
+
+int rows_mode_ok(const char* who, const void* k, const int64_t* k_strides, const void* v,
+                 const int64_t* v_strides, const int32_t* key_lengths, int64_t key_tokens) {
+  static thread_local std::string msg;
+  if (!operand_ok(k, k_strides, false) || !operand_ok(v, v_strides, false) ||
+      !rows_mode_possible(nullptr, key_lengths, key_tokens, k_strides, v_strides)) {
+    msg = std::string(who) +
+          ": without tiles, K and V must be 16-byte aligned strided rows (token stride < 2^24 elements), "
+          "key_lengths NULL and key_tokens >= 64";
+    return fail(SOL_ERR_INVALID, msg.c_str());
+  }
+  return SOL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -135,7 +158,7 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
     return err(SOL_ERR_INVALID, "chunk_sums, key_mean and key_var go together (with ctiles)");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
   if (nkb > (int64_t(1) << 19)) return err(SOL_ERR_UNSUPPORTED, "too many key blocks");
-  sol::PoolParams p;
+  sol::PoolParams p{};
   p.k = rows_of(k, k_strides, key_index, key_tokens, sequence_length);
   p.v = rows_of(v, v_strides, key_index, key_tokens, sequence_length);
   p.klen = key_lengths;
@@ -185,7 +208,7 @@ int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* que
     return fail(SOL_ERR_INVALID, "sol_pair_strides: workspace (16-byte aligned) and strides are required");
   if (query_index && sequence_length <= 0)
     return fail(SOL_ERR_INVALID, "sol_pair_strides: an indexed Q needs sequence_length > 0");
-  sol::PairParams p;
+  sol::PairParams p{};
   p.q = rows_of(q, q_strides, query_index, query_tokens, sequence_length);
   p.B = int(batch);
   p.H = int(heads);
@@ -206,7 +229,7 @@ int sol_plan_protection(const int64_t* rows, const int64_t* keys, const int32_t*
     return fail(SOL_ERR_INVALID, "sol_plan_protection: invalid shape or range count");
   if (!rows || !keys || !protected_blocks || (nranges > 0 && !ranges))
     return fail(SOL_ERR_INVALID, "sol_plan_protection: rows, keys, ranges and protected_blocks are required");
-  sol::PlanParams p;
+  sol::PlanParams p{};
   p.rows = rows;
   p.keys = keys;
   p.key_lengths = key_lengths;
@@ -239,7 +262,7 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
   if (nkb > SOL_MAX_KEY_BLOCKS)
     return fail(SOL_ERR_UNSUPPORTED, "sol_key_covariance: key_tokens exceeds 64 * SOL_MAX_KEY_BLOCKS");
-  sol::CovParams p;
+  sol::CovParams p{};
   p.ctiles = static_cast<const uint16_t*>(ctiles);
   p.mean = key_mean;
   p.klen = key_lengths;
@@ -256,6 +279,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       int64_t sequence_length, int64_t batch, int64_t query_tokens,
                       int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,
+                      const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                       const void* tiles, const void* ctiles, const float* key_mean,
                       const float* key_var, const float* key_cov, const uint8_t* protection,
                       const int32_t* pair_strides, double scale, double beta,
@@ -271,20 +295,22 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: Q needs 16-byte aligned rows and positive strides");
   if ((query_index || out_index) && sequence_length <= 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_index / out_index need sequence_length > 0");
-  if (workgroup_form < 0 || workgroup_form > 3)
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: workgroup_form must be 0, 1, 2 or 3");
+  if (workgroup_form < 0 || workgroup_form > 2)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: workgroup_form must be 0, 1 or 2");
   if ((qk_int8_tiles == nullptr) != (qk_int8_scales == nullptr) || (qk_int8_tiles && !aligned16(qk_int8_tiles)))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: qk_int8_tiles (16-byte aligned) and qk_int8_scales go together");
-  if (qk_int8_tiles && workgroup_form == 3)
-    return fail(SOL_ERR_UNSUPPORTED, "sol_attention_fwd: the INT8 QK experiment runs in workgroup forms 0, 1 and 2");
   if (!std::isfinite(scale) || scale <= 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: scale must be finite and positive");
   if (std::isnan(beta)) return fail(SOL_ERR_INVALID, "sol_attention_fwd: beta must not be NaN");
   if (kv_sink_tokens < 0 || query_sink_tokens < 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: sink token counts must be nonnegative");
   const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
-  if (!tiles || !ctiles || !aligned16(tiles) || !aligned16(ctiles) || !out || !aligned16(out))
+  if (!ctiles || !aligned16(ctiles) || !out || !aligned16(out) || (tiles && !aligned16(tiles)))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: tiles/ctiles/out must be 16-byte aligned device buffers");
+  if (!tiles) {
+    const int rc = rows_mode_ok("sol_attention_fwd", k, k_strides, v, v_strides, key_lengths, key_tokens);
+    if (rc != SOL_OK) return rc;
+  }
   if (force == 0 && (!key_mean || !key_var))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
@@ -304,6 +330,10 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   p.k8 = static_cast<const int8_t*>(qk_int8_tiles);
   p.k8_scale = qk_int8_scales;
   p.tiles = static_cast<const uint16_t*>(tiles);
+  if (!tiles) {
+    p.k = rows_of(k, k_strides, nullptr, key_tokens);
+    p.v = rows_of(v, v_strides, nullptr, key_tokens);
+  }
   p.ctiles = static_cast<const uint16_t*>(ctiles);
   p.mean = key_mean;
   p.var = key_var;
@@ -332,19 +362,33 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   return hip_status(sol::launch_sol(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
-int sol_quantize_keys(const void* tiles, int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
-                      void* k8_tiles, float* k8_scales, void* stream) {
+int sol_quantize_keys(const void* k, const int64_t* k_strides, const int64_t* key_index,
+                      const int32_t* key_lengths, int64_t sequence_length, int64_t batch, int64_t key_tokens,
+                      int64_t heads, int64_t head_dim, int rows_mode, void* k8_tiles, float* k8_scales,
+                      void* stream) {
   if (!shape_ok(batch, key_tokens, heads, head_dim))
     return fail(SOL_ERR_INVALID, "sol_quantize_keys: unsupported shape (head_dim must be 64 or 128)");
-  if (!tiles || !k8_tiles || !k8_scales || !aligned16(tiles) || !aligned16(k8_tiles))
-    return fail(SOL_ERR_INVALID, "sol_quantize_keys: tiles and k8_tiles (16-byte aligned) and k8_scales are required");
+  if (!operand_ok(k, k_strides, key_index != nullptr))
+    return fail(SOL_ERR_INVALID, "sol_quantize_keys: K needs 16-byte aligned rows and positive strides");
+  if (key_index && sequence_length <= 0)
+    return fail(SOL_ERR_INVALID, "sol_quantize_keys: an indexed source needs sequence_length > 0");
+  if (!k8_tiles || !k8_scales || !aligned16(k8_tiles))
+    return fail(SOL_ERR_INVALID, "sol_quantize_keys: k8_tiles (16-byte aligned) and k8_scales are required");
+  if (rows_mode && (key_index || key_lengths || key_tokens < SOL_BLOCK))
+    return fail(SOL_ERR_INVALID, "sol_quantize_keys: rows_mode needs plain K rows (no index, no key_lengths) "
+                                 "and key_tokens >= 64");
   const int64_t ntiles = batch * heads * cdiv(key_tokens, SOL_BLOCK);
   if (ntiles >= (int64_t(1) << 31)) return fail(SOL_ERR_UNSUPPORTED, "sol_quantize_keys: grid too large");
-  sol::QuantParams p;
-  p.tiles = static_cast<const uint16_t*>(tiles);
+  sol::QuantParams p{};
+  p.k = rows_of(k, k_strides, key_index, key_tokens, sequence_length);
+  p.klen = key_lengths;
   p.k8 = static_cast<int8_t*>(k8_tiles);
   p.scale = k8_scales;
-  p.ntiles = ntiles;
+  p.B = int(batch);
+  p.H = int(heads);
+  p.Tk = int(key_tokens);
+  p.NKB = int(cdiv(key_tokens, SOL_BLOCK));
+  p.shifted = rows_mode ? 1 : 0;
   return hip_status(sol::launch_quantize_keys(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
@@ -362,14 +406,27 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
   if (!out || !aligned16(out)) return fail(SOL_ERR_INVALID, "sol_dense_fwd: out must be 16-byte aligned");
   if (batch * heads * cdiv(query_tokens, 128) >= (int64_t(1) << 31))
     return fail(SOL_ERR_UNSUPPORTED, "sol_dense_fwd: grid too large");
-  const int rc = pool_checked("sol_dense_fwd", k, k_strides, v, v_strides, nullptr, nullptr, 0, batch,
-                              key_tokens, heads, head_dim, nullptr, tiles, nullptr, nullptr,
-                              nullptr, stream);
-  if (rc != SOL_OK) return rc;
+  // Key blocks straight from K / V rows, or (fewer than 64 keys, or token
+  // strides too large for rows mode) from tiles pooled into the workspace.
+  const bool rows = rows_mode_possible(nullptr, nullptr, key_tokens, k_strides, v_strides);
+  if (rows) {
+    const int rc = rows_mode_ok("sol_dense_fwd", k, k_strides, v, v_strides, nullptr, key_tokens);
+    if (rc != SOL_OK) return rc;
+  } else {
+    if (!tiles) return fail(SOL_ERR_INVALID, "sol_dense_fwd: this shape needs the tiles workspace");
+    const int rc = pool_checked("sol_dense_fwd", k, k_strides, v, v_strides, nullptr, nullptr, 0, batch,
+                                key_tokens, heads, head_dim, nullptr, tiles, nullptr, nullptr,
+                                nullptr, stream);
+    if (rc != SOL_OK) return rc;
+  }
   sol::AttnParams p;
   std::memset(&p, 0, sizeof(p));
   p.q = rows_of(q, q_strides, nullptr, query_tokens);
-  p.tiles = static_cast<const uint16_t*>(tiles);
+  p.tiles = rows ? nullptr : static_cast<const uint16_t*>(tiles);
+  if (rows) {
+    p.k = rows_of(k, k_strides, nullptr, key_tokens);
+    p.v = rows_of(v, v_strides, nullptr, key_tokens);
+  }
   p.out = static_cast<uint16_t*>(out);
   p.B = int(batch);
   p.H = int(heads);
@@ -394,8 +451,11 @@ int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k
   int64_t sizes[4];
   if (sol_pool_sizes(batch, key_tokens, heads, head_dim, sizes) != SOL_OK) return SOL_ERR_INVALID;
   const bool moments = std::isfinite(beta);
+  // Rows mode needs no block tiles; fewer than 64 keys (or huge token
+  // strides) take them in the workspace.
+  const bool rows = rows_mode_possible(nullptr, nullptr, key_tokens, k_strides, v_strides);
   const int64_t off_tiles = align256(sizes[0]);
-  const int64_t off_sums = off_tiles + align256(sizes[1]);
+  const int64_t off_sums = off_tiles + (rows ? 0 : align256(sizes[1]));
   const int64_t off_mean = off_sums + align256(sizes[2]);
   const int64_t off_var = off_mean + align256(sizes[3]);
   const int64_t need = moments ? off_var + align256(sizes[3]) : off_sums;
@@ -410,11 +470,13 @@ int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k
   float* sums = moments ? reinterpret_cast<float*>(ws + off_sums) : nullptr;
   float* mean = moments ? reinterpret_cast<float*>(ws + off_mean) : nullptr;
   float* var = moments ? reinterpret_cast<float*>(ws + off_var) : nullptr;
+  void* tiles = rows ? nullptr : ws + off_tiles;
   const int prc = pool_checked("sol_attention_noalloc", k, k_strides, v, v_strides, nullptr, nullptr, 0, batch,
-                               key_tokens, heads, head_dim, ws, ws + off_tiles, sums, mean, var, stream);
+                               key_tokens, heads, head_dim, ws, tiles, sums, mean, var, stream);
   if (prc != SOL_OK) return prc;
   return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
-                           head_dim, ws + off_tiles, ws, mean, var, nullptr, nullptr, nullptr, scale, beta,
+                           head_dim, k, k_strides, v, v_strides, tiles, ws, mean, var, nullptr, nullptr, nullptr,
+                           scale, beta,
                            local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr, counts, nullptr,
                            nullptr, nullptr, nullptr, nullptr, 0, stream);
 }

@@ -5,9 +5,12 @@
 // row is read exactly once with 16-byte loads (through the index for indexed
 // windows); the outputs are written in the layouts the attention kernels use:
 //   ctiles [B, H, NCT, 2, 64 D] BF16 block centroids, 64 key blocks per tile,
-//                          as a swizzled K / V^T tile pair (TileLayout);
+//                          as a swizzled K / V tile pair (TileLayout);
 //                          NCT = ceil(NKB / 64), zero beyond the last block
-//   tiles  [B, H, NKB, 2, 64 D] swizzled K and V^T token tiles per key block
+//   tiles  [B, H, NKB, 2, 64 D] K and V token tiles per key block, only for
+//                          keys the attention kernels cannot DMA row by row
+//                          straight from K and V (indexed or ragged windows,
+//                          fewer than 64 keys)
 // Both are streamed into LDS by the attention kernels with DMA.
 // Sums follow torch's CPU outer-reduction order (16-row sequential chunks,
 // folded in order), so the FP32 means and the BF16-rounded centroids equal the
@@ -22,16 +25,18 @@
 namespace sol {
 
 // Two workgroup forms, both covering one 16-block chunk per workgroup:
-// - NW = 4 waves, each pooling 4 blocks in turn (large grids).  One wave per
-//   SIMD: each wave keeps 16 rows x 16 bytes per lane in flight, so one
-//   workgroup per CU already has ~16 MB of reads outstanding chip-wide.  More
-//   waves only deepen the memory queues: the pass measured 0.50 ms at 3 waves
-//   per SIMD, 0.47 ms at 2 and 0.42 ms at 1 (same code otherwise).
+// - NW = 4 waves, each pooling 4 blocks in turn (large grids), each keeping
+//   16 rows x 16 bytes per lane in flight, with non-temporal loads (K and V
+//   are streamed once here).  Two waves per SIMD: at 84,672 tokens x 24
+//   heads the read-only pass measured 0.231 ms at one wave per SIMD, 0.207
+//   at two, 0.210 at three, and 0.172 with two and non-temporal loads;
+//   issuing the next block's loads before summing the current one (two
+//   blocks in flight per wave) did not help (0.210).
 // - NW = 16 / BPI waves, one block (D = 128) or two (D = 64) each, all in
 //   flight at once (grids too small to fill the GPU, where the four
 //   sequential rounds of the first form are the whole run time).
 template <int D, int NW>
-__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(1, NW == 4 ? 1 : NW / 4)))
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(1, NW == 4 ? 2 : NW / 4)))
 void pool_kv_kernel(PoolParams p) {
   constexpr int DC = D / 8;          // 16-byte chunks per token row
   constexpr int LPB = DC * 4;        // lanes per key block: 4 chunks of 16 rows
@@ -66,31 +71,15 @@ void pool_kv_kernel(PoolParams p) {
     if (j < nkb) {
       len = min(kBlock, tk - kBlock * j);
       u32x4 x[16];
-      load_rows16(src, b, kBlock * j + 16 * r4, kBlock * j + len - 1, h, 8 * dc, x);
+      load_rows16<16, true>(src, b, kBlock * j + 16 * r4, kBlock * j + len - 1, h, 8 * dc, x);
       if (p.tiles) {
-        // Attention-ready tiles: K rows as loaded, V transposed 8x8 in registers.
+        // Attention-ready tiles in the LDS image layout (zero past the end),
+        // for keys the attention kernels cannot DMA row by row.
         uint16_t* tile = p.tiles + ((int64_t(b) * p.H + h) * p.NKB + j) * 2 * TL::kElems;
-        if (!is_v) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i)
-            *reinterpret_cast<u32x4*>(tile + TL::k_offset(16 * r4 + i, dc)) = x[i];
-        } else {
-          // A Vᵀ chunk holds 4-key groups g and g + 2 of one feature, so the
-          // 8x8 transpose takes rows 16 r4 + 4 sb + {0..3, 8..11}: each
-          // transposed row is then one whole 16-byte chunk (group 4 r4 + sb
-          // in its low half, 4 r4 + sb + 2 in its high half).
-          uint16_t* vt = tile + TL::kElems;
-#pragma unroll
-          for (int sb = 0; sb < 2; ++sb) {
-            u32x4 rows[8], cols[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) rows[i] = x[4 * sb + (i < 4 ? i : i + 4)];
-            transpose8x8(rows, cols);
-            const int g = 4 * r4 + sb;
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-              *reinterpret_cast<u32x4*>(vt + TL::vt_offset(8 * dc + e, g)) = cols[e];
-          }
+        for (int i = 0; i < 16; ++i) {
+          const int row = 16 * r4 + i;
+          *reinterpret_cast<u32x4*>(tile + (is_v ? TL::kElems + TL::v_offset(row, dc) : TL::k_offset(row, dc))) = x[i];
         }
       }
       // Sequential accumulation inside the 16-row chunk (torch order).
@@ -132,7 +121,7 @@ void pool_kv_kernel(PoolParams p) {
 
   const int64_t head = int64_t(b) * p.H + h;
   if (!p.ctiles) return;  // tiles only (dense path)
-  // Centroid tiles: 64 consecutive key blocks per tile, laid out like a K / V^T
+  // Centroid tiles: 64 consecutive key blocks per tile, laid out like a K / V
   // tile pair.  This chunk fills rows r0 .. r0 + 15 of tile ct.
   const int ct = (c * kPoolChunk) / kBlock;
   const int r0 = (c * kPoolChunk) % kBlock;
@@ -157,13 +146,10 @@ void pool_kv_kernel(PoolParams p) {
       dst[tid] = s1;
       dst[D + tid] = s2;
     }
-  } else {
-    for (int idx = tid; idx < 4 * D; idx += NT) {
-      const int d = idx >> 2, gq = idx & 3;  // 4-centroid group gq of this chunk
-      const u32x2 o = {uint32_t(cent[4 * gq][d]) | (uint32_t(cent[4 * gq + 1][d]) << 16),
-                       uint32_t(cent[4 * gq + 2][d]) | (uint32_t(cent[4 * gq + 3][d]) << 16)};
-      *reinterpret_cast<u32x2*>(ctile + TL::kElems + TL::vt_offset(d, r0 / 4 + gq)) = o;
-    }
+  } else if (tid < kPoolChunk * DC) {
+    const int jb = tid / DC, cc = tid % DC;
+    *reinterpret_cast<u32x4*>(ctile + TL::kElems + TL::v_offset(r0 + jb, cc)) =
+        *reinterpret_cast<const u32x4*>(&cent[jb][8 * cc]);
   }
 }
 

@@ -2,11 +2,15 @@
 // (ROADMAP.md:14-16: "separately measured INT8 QK ... Preserve a BF16
 // control"), which the reference does not implement.
 //
-// Per key block (64 keys x D, one BF16 K tile of the pooling pass): one
-// symmetric scale s_k = max|K| / 127 over the block, K8 = rint(K * (127 /
-// max|K|)) clamped to +-127 (0 for an all-zero block), stored in the
-// bank-swizzled K8Layout the attention kernel's INT8 products read.  HBM-bound:
-// 16 KB read and 8 KB + 4 bytes written per block.
+// Per key block (64 keys x D): one symmetric scale s_k = max|K| / 127 over
+// the block's keys, K8 = rint(K * (127 / max|K|)) clamped to +-127 (0 for an
+// all-zero block), stored in the bank-swizzled K8Layout the attention
+// kernel's INT8 products read, with the block's rows where the attention
+// kernels' BF16 V tile has them: rows 64 j .. of the sequence, zero past its
+// end, or -- for the partial last block of a sequence whose V rows the
+// attention kernel reads shifted back (p.shifted) -- the sequence's last 64
+// rows, of which only the block's own keys (the last len) set the scale.
+// HBM-bound: D * 128 bytes read and D * 64 + 4 written per block.
 #include "sol_device.h"
 #include "sol_internal.h"
 
@@ -18,16 +22,23 @@ constexpr int kQuantThreads = 256;
 
 template <int D>
 __global__ __launch_bounds__(kQuantThreads) void quantize_keys_kernel(QuantParams p) {
-  using TL = TileLayout<D>;
   constexpr int kChunks = kBlock * D / 16;  // INT8 chunks (16 features) per block
   constexpr int kPer = kChunks / kQuantThreads;
   constexpr int kRowChunks = D / 16;
   static_assert(kPer * kQuantThreads == kChunks, "chunks split evenly over the workgroup");
   __shared__ float s_max[kQuantThreads / kWave];
 
-  const int64_t tile = blockIdx.x;
-  const uint16_t* src = p.tiles + tile * int64_t(2 * TL::kElems);  // the block's K half
-  int8_t* dst = p.k8 + tile * int64_t(K8Layout<D>::kBytes);
+  const int j = blockIdx.x % p.NKB;
+  const int bh = blockIdx.x / p.NKB;
+  const int h = bh % p.H, b = bh / p.H;
+  const int tk = batch_tokens(p.klen, b, p.Tk);
+  const int nkb = (tk + kBlock - 1) / kBlock;
+  if (j >= nkb) return;  // past this entry's blocks (uniform per workgroup)
+  const int len = min(kBlock, tk - kBlock * j);
+  const bool shifted = p.shifted && len < kBlock;
+  const int row0 = shifted ? tk - kBlock : kBlock * j;  // sequence row of tile row 0
+  const int first = shifted ? kBlock - len : 0;          // tile rows first .. first + len - 1 are the block's
+  int8_t* dst = p.k8 + int64_t(blockIdx.x) * K8Layout<D>::kBytes;
   const int tid = threadIdx.x, lane = tid & 63;
 
   u32x4 raw[kPer][2];
@@ -36,13 +47,18 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_keys_kernel(QuantParam
   for (int i = 0; i < kPer; ++i) {
     const int c = tid + kQuantThreads * i;
     const int row = c / kRowChunks, ch = c % kRowChunks;
+    const bool present = row >= first && row < first + len;
+    const bool readable = shifted || present;  // shifted rows all exist
+    const uint16_t* src = p.k.row(b, row0 + (readable ? row : first), h) + 16 * ch;
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      raw[i][hf] = load16(src + TL::k_offset(row, 2 * ch + hf));
+      raw[i][hf] = readable ? load16(src + 8 * hf) : zero_u32x4();
+      if (present) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t w = raw[i][hf][e >> 1];
-        amax = fmaxf(amax, fabsf(bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu))));
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t w = raw[i][hf][e >> 1];
+          amax = fmaxf(amax, fabsf(bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu))));
+        }
       }
     }
   }
@@ -75,16 +91,17 @@ __global__ __launch_bounds__(kQuantThreads) void quantize_keys_kernel(QuantParam
     }
     *reinterpret_cast<u32x4*>(dst + K8Layout<D>::offset(row, ch)) = out;
   }
-  if (tid == 0) p.scale[tile] = __fdiv_rn(amax, 127.f);
+  if (tid == 0) p.scale[blockIdx.x] = __fdiv_rn(amax, 127.f);
 }
 
 }  // namespace
 
 hipError_t launch_quantize_keys(const QuantParams& p, int D, hipStream_t stream) {
+  const dim3 grid(unsigned(int64_t(p.B) * p.H * p.NKB));
   if (D == 128)
-    hipLaunchKernelGGL(quantize_keys_kernel<128>, dim3(unsigned(p.ntiles)), dim3(kQuantThreads), 0, stream, p);
+    hipLaunchKernelGGL(quantize_keys_kernel<128>, grid, dim3(kQuantThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL(quantize_keys_kernel<64>, dim3(unsigned(p.ntiles)), dim3(kQuantThreads), 0, stream, p);
+    hipLaunchKernelGGL(quantize_keys_kernel<64>, grid, dim3(kQuantThreads), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -10,7 +10,8 @@
 // Scores are computed transposed, S^T = K * Q^T, so each lane owns ONE query
 // (its C column) and the softmax row statistics never leave the lane pair
 // (l, l ^ 32).  P^T then feeds O^T = V^T * P^T as the B operand straight
-// from registers; only V needs a transposed (key-contiguous) LDS tile.
+// from registers; the V^T operand is read from row-major V tiles with the
+// LDS transpose read ds_read_b64_tr_b16.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -112,8 +113,8 @@ __device__ __forceinline__ u32x4 load16(const uint16_t* p) {
 // first (the index entries of an indexed source all in flight together) and
 // every data load is then issued unconditionally -- rows past t_last re-read
 // row t_last -- so the N loads are in flight at once instead of each waiting
-// behind a branch.
-template <int N>
+// behind a branch.  STREAM marks the loads non-temporal (data read once).
+template <int N, bool STREAM = false>
 __device__ __forceinline__ void load_rows16(const TokenRows& r, int b, int t0, int t_last, int h, int col,
                                             u32x4 (&x)[N]) {
   const uint16_t* p[N];
@@ -130,7 +131,8 @@ __device__ __forceinline__ void load_rows16(const TokenRows& r, int b, int t0, i
     for (int i = 0; i < N; ++i) p[i] = base + int64_t(min(t0 + i, t_last)) * r.st;
   }
 #pragma unroll
-  for (int i = 0; i < N; ++i) x[i] = load16(p[i]);
+  for (int i = 0; i < N; ++i)
+    x[i] = STREAM ? __builtin_nontemporal_load((global_u32x4_ptr)(p[i])) : load16(p[i]);
 #pragma unroll
   for (int i = 0; i < N; ++i)
     if (t0 + i > t_last) x[i] = zero_u32x4();
@@ -140,64 +142,40 @@ __device__ __forceinline__ u32x2 load8(const uint16_t* p) {
   return *reinterpret_cast<const u32x2*>(p);
 }
 
-// 8x8 bf16 transpose of eight 16-byte rows: out[d] packs rows 0..7 of column d.
-__device__ __forceinline__ void transpose8x8(const u32x4 (&in)[8], u32x4 (&out)[8]) {
-#pragma unroll
-  for (int d = 0; d < 8; ++d) {
-#pragma unroll
-    for (int kp = 0; kp < 4; ++kp) {
-      const uint32_t lo = in[2 * kp][d / 2];
-      const uint32_t hi = in[2 * kp + 1][d / 2];
-      out[d][kp] = (d & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u))
-                           : ((lo & 0xFFFFu) | (hi << 16));
-    }
-  }
-}
-
-// Block tiles written by the pooling pass and streamed by the attention kernels.
-// Per (batch, head, key block): a K tile (64 keys x D, row-major) followed by a
-// V^T tile (D features x 64 keys), one contiguous copy each.  Both are
-// swizzled so that the MFMA operand reads from LDS hit distinct banks whether
-// the LDS serves 128 or 256 bytes per clock (32 or 64 four-byte banks):
-//   K tile:   16-byte chunk c of key row r sits at chunk c ^ s_k(r), where
-//             s_k(r) = r & 15 for 256-byte rows (D = 128) and (r >> 1) & 7 for
-//             128-byte rows (D = 64); 16 consecutive rows (one 16-lane phase of
-//             a ds_read_b128) then cover all banks.
-//   V^T tile: a feature row (64 keys, 128 bytes) is 8 chunks of 16 bytes, one
-//             per MFMA A fragment: chunk c = 4 t + 2 c4 + hh holds the 4-key
-//             groups 8 t + 4 c4 + hh (low half) and that + 2 (high half), the
-//             keys lane half hh supplies for 16-key step c4 of 32-key half t
-//             (the k-slot order of the score MFMA's result).  Chunk c of row d
-//             sits at chunk c ^ s_v(d), s_v(d) = (d & 7) ^ ((d >> 3) & 1): 8
-//             consecutive rows use 8 distinct chunks and 16 consecutive rows
-//             distinct (row parity, chunk) pairs.
-// Keys past the end of the sequence are zero in both tiles.
+// Key-block tiles as the attention kernels hold them in LDS (and as the
+// pooling pass writes the centroid tiles and, for indexed windows, the
+// gathered key blocks): per key block a K tile then a V tile, 64 key rows x D
+// BF16 features each, in 16-byte chunks (8 features) placed so that the MFMA
+// operand reads hit distinct LDS banks (64 banks of 4 bytes):
+//   K: row-major; chunk c of row r sits at chunk c ^ s_k(r) of the row,
+//      s_k(r) = r & 15 for 256-byte rows (D = 128) and (r >> 1) & 7 for
+//      128-byte rows (D = 64): the 16 rows of one 16-lane ds_read_b128
+//      phase (a score operand) cover all banks.
+//   V: row quads; the 4 rows 4 q .. 4 q + 3 fill chunks 4 q CPR ..
+//      4 (q + 1) CPR (CPR = D / 8 chunks per row) ordered (c >> 2, r & 3,
+//      c & 3).  The P V operand (32 features x 8 keys per lane) is read with
+//      ds_read_b64_tr_b16, which gives a lane 4 consecutive keys of one
+//      feature: one 32-lane half of a read takes the 4 rows of one quad at
+//      4 chunks each, 256 contiguous bytes (all 64 banks), and every part of
+//      the address but the lane's own is an immediate.
+// Keys past the end of the sequence are zero in the tiles the pooling pass
+// writes; kernels that DMA key rows straight from the caller's tensors repeat
+// the last valid row there (and mask those keys out of the softmax).
 template <int D>
 struct TileLayout {
-  static constexpr int kElems = kBlock * D;   // elements per K (or V^T) tile
-  __device__ static __forceinline__ int k_offset(int row, int chunk) {
-    const int sw = D == 128 ? (row & 15) : ((row >> 1) & 7);
-    return row * D + 8 * (chunk ^ sw);
+  static constexpr int kElems = kBlock * D;  // elements of one K (or V) tile
+  static constexpr int kRowChunks = D / 8;
+  __device__ static __forceinline__ int k_swizzle(int row) { return D == 128 ? (row & 15) : ((row >> 1) & 7); }
+  // Element offsets (inside the K tile, and inside the V tile) of chunk c of row r.
+  __device__ static __forceinline__ int k_offset(int row, int chunk) { return row * D + 8 * (chunk ^ k_swizzle(row)); }
+  __device__ static __forceinline__ int v_offset(int row, int chunk) {
+    return 8 * ((row >> 2) * 4 * kRowChunks + (chunk >> 2) * 16 + (row & 3) * 4 + (chunk & 3));
   }
-  // V^T swizzle of feature row d.
-  __device__ static __forceinline__ int vt_swizzle(int d) { return (d & 7) ^ ((d >> 3) & 1); }
-  // Element offset of 16-byte fragment chunk c of feature row d.
-  __device__ static __forceinline__ int vt_chunk(int d, int c) { return d * kBlock + 8 * (c ^ vt_swizzle(d)); }
-  // The MFMA operand reads as (lane part) + (XOR part ^ per-read constant):
+  // The score operand read as (lane part) + (XOR part ^ per-read constant):
   // for key row r = 32 t + col and chunk c = 2 ks + hh,
   //   k_offset(r, c) = r D + (k_lane_xor(col, hh) ^ 16 ks),
-  // and for feature row d = 32 dt + col and chunk c = 4 t + 2 c4 + hh,
-  //   vt_chunk(d, c) = d 64 + (vt_lane_xor(col, hh) ^ (32 t + 16 c4)),
-  // since the swizzles depend only on col and 2 ks, 4 t + 2 c4 leave bit 0 free.
-  __device__ static __forceinline__ int k_lane_xor(int col, int hh) {
-    const int sw = D == 128 ? (col & 15) : ((col >> 1) & 7);
-    return 8 * (hh ^ sw);
-  }
-  __device__ static __forceinline__ int vt_lane_xor(int col, int hh) { return 8 * (hh ^ vt_swizzle(col)); }
-  // Element offset of 4-key group g (keys 4 g .. 4 g + 3) of feature row d.
-  __device__ static __forceinline__ int vt_offset(int d, int g) {
-    return vt_chunk(d, 2 * (g >> 2) + (g & 1)) + 4 * ((g >> 1) & 1);
-  }
+  // since s_k depends only on col and 2 ks leaves bit 0 free.
+  __device__ static __forceinline__ int k_lane_xor(int col, int hh) { return 8 * (hh ^ k_swizzle(col)); }
 };
 
 // INT8 K tiles of the quantised-QK experiment: per key block 64 rows x D

@@ -19,8 +19,8 @@ __device__ __forceinline__ int batch_tokens(const int32_t* klen, int b, int T) {
 struct PoolParams {
   TokenRows k, v;
   const int32_t* klen;  // [B] key tokens per batch entry (<= Tk), or null: all Tk
-  uint16_t* ctiles;  // [B, H, NCT, 2, 64 * D] centroid tiles, or null (tiles only)
-  uint16_t* tiles;   // [B, H, NKB, 2, 64 * D] swizzled K / V^T block tiles, or null
+  uint16_t* ctiles;  // [B, H, NCT, 2, 64 * D] centroid tiles, or null
+  uint16_t* tiles;   // [B, H, NKB, 2, 64 * D] K / V block tiles (TileLayout), or null
   float* ksum;       // [B, H, NCH, 2, D] chunk sums, null -> no moments
   float* mean;       // [B, H, D]
   float* var;        // [B, H, D]
@@ -59,7 +59,8 @@ struct AttnParams {
   const int32_t* klen;         // [B] key tokens per batch entry (<= Tk), or null: all Tk
   const int64_t* out_index;    // [B, Tq] output rows of an [N, H, D] output, or null
   int64_t out_rows;            // N: rows of an out_index output (others are skipped)
-  const uint16_t* tiles;       // [B, H, NKB, 2, 64 * D] from the pooling pass
+  TokenRows k, v;              // key rows the kernels DMA straight into LDS (tiles null)
+  const uint16_t* tiles;       // [B, H, NKB, 2, 64 * D] pooled block tiles, or null: rows of k / v
   const uint16_t* ctiles;      // [B, H, NCT, 2, 64 * D] centroid tiles
   const float* mean;           // [B, H, D]
   const float* var;            // [B, H, D]
@@ -78,7 +79,7 @@ struct AttnParams {
   int local_blocks;   // < 0 disables the local band
   int kv_sink_blocks, q_sink_blocks;
   int workgroup_form;  // 0: by launch size; 1 / 2: query blocks per workgroup of
-                       // sol_attention_kernel; 3: the ping-pong kernel (two blocks)
+                       // sol_attention_kernel
 };
 
 // Indexed-window protection (plan.hip).
@@ -94,17 +95,17 @@ struct PlanParams {
 
 // INT8 K tiles of the quantised-QK experiment (quant.hip).
 struct QuantParams {
-  const uint16_t* tiles;  // [B, H, NKB, 2, 64 * D] BF16 tile pairs (K halves read)
-  int8_t* k8;             // [B, H, NKB, 64 * D]
-  float* scale;           // [B, H, NKB]
-  int64_t ntiles;         // B * H * NKB
+  TokenRows k;
+  const int32_t* klen;  // [B] key tokens per batch entry (<= Tk), or null: all Tk
+  int8_t* k8;           // [B, H, NKB, 64 * D]
+  float* scale;         // [B, H, NKB]
+  int B, H, Tk, NKB;
+  int shifted;          // partial last blocks as the rows-mode attention tiles hold them
 };
 
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream);
 hipError_t launch_quantize_keys(const QuantParams& p, int D, hipStream_t stream);
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream);
-hipError_t launch_sol_pp(const AttnParams& p, int D, hipStream_t stream);
-hipError_t launch_dense_pp(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_dense(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream);
 hipError_t launch_plan_protection(const PlanParams& p, hipStream_t stream);

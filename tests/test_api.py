@@ -144,7 +144,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == 7
+    assert native.sol_abi_version() == _native.ABI_VERSION == 8
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -167,14 +167,23 @@ def test_c_abi_rejects_bad_arguments_without_launching():
                               float("nan"), fake, fake, None)
     assert rc == -1 and b"scale" in native.sol_last_error()
     attn = lambda index, n, form: native.sol_attention_fwd(  # noqa: E731
-        fake, strides, index, n, 1, 193, 317, None, 2, 64, fake, fake, fake, fake, None, None, None,
-        0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, form, None)
-    rc = native.sol_attention_fwd(fake, strides, None, 0, 1, 193, 317, None, 2, 64, fake, fake,
-                                  None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None,
-                                  None, None, None, None, None, 0, None)
+        fake, strides, index, n, 1, 193, 317, None, 2, 64, None, None, None, None, fake, fake, fake, fake,
+        None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, form, None)
+    rc = native.sol_attention_fwd(fake, strides, None, 0, 1, 193, 317, None, 2, 64, None, None, None, None,
+                                  fake, fake, None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None,
+                                  None, None, None, None, None, None, 0, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
-    assert attn(None, 0, 4) == -1 and b"workgroup_form" in native.sol_last_error()
+    assert attn(None, 0, 3) == -1 and b"workgroup_form" in native.sol_last_error()
     assert attn(fake, 0, 0) == -1 and b"sequence_length" in native.sol_last_error()
+    # Without tiles the keys must qualify for rows mode.
+    rows = lambda nk, lengths: native.sol_attention_fwd(  # noqa: E731
+        fake, strides, None, 0, 1, 193, nk, lengths, 2, 64, fake, strides, fake, strides, None, fake,
+        fake, fake, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, 0,
+        None)
+    assert rows(63, None) == -1 and b"without tiles" in native.sol_last_error()
+    assert rows(317, fake) == -1 and b"without tiles" in native.sol_last_error()
+    rc = native.sol_quantize_keys(fake, strides, None, None, 0, 1, 40, 2, 64, 1, fake, fake, None)
+    assert rc == -1 and b"rows_mode" in native.sol_last_error()
     rc = native.sol_pair_strides(fake, strides, None, 0, 1, 192, 2, 64, fake, fake, None)
     assert rc == -2 and b"4 .. 8192 query blocks" in native.sol_last_error()
     rc = native.sol_pair_strides(fake, strides, None, 0, 1, 193, 2, 64, None, fake, None)
@@ -211,10 +220,11 @@ def test_noalloc_rejects_problems_beyond_its_workspace_without_launching():
     if not os.path.exists(_native.LIB_PATH):
         pytest.skip("libsol_attn_amd.so not built")
     native = _native.library()
-    strides = (ctypes.c_int64 * 3)(16 * 128 * 20000, 16 * 128, 128)
+    tk = 64 * 8192
+    strides = (ctypes.c_int64 * 3)(64 * 128 * tk, 64 * 128, 128)
     fake = ctypes.c_void_p(1 << 20)   # never dereferenced: the size check fails first
-    # 1 x 20,000 keys x 16 heads at D = 128 needs about 160 MiB of pooled keys.
-    rc = native.sol_attention_noalloc(fake, strides, fake, strides, fake, strides, 1, 20000, 20000, 16, 128,
+    # 524,288 keys x 64 heads at D = 128: 256 MiB of centroid tiles.
+    rc = native.sol_attention_noalloc(fake, strides, fake, strides, fake, strides, 1, 200, tk, 64, 128,
                                       0.088, 1.0, 1, 0, 0, fake, None, None)
     assert rc == -2 and b"SOL_NOALLOC_SCRATCH_BYTES" in native.sol_last_error()
     rc = native.sol_attention_noalloc(fake, strides, fake, strides, fake, strides, 1, 200, 200, 16, 96,

@@ -73,7 +73,7 @@ def _ragged_case(seed, n=1500, heads=2, d=128):
     return x, rows, keys
 
 
-@pytest.mark.parametrize("group", ["1", "2", "3"])  # one- and two-block workgroups
+@pytest.mark.parametrize("group", ["1", "2"])  # one- and two-block workgroups
 @pytest.mark.parametrize("beta", [-math.inf, math.inf, 1.0, 0.0])
 def test_ragged_windows_one_call_equal_separate_calls_and_oracle(beta, group, monkeypatch):
     monkeypatch.setattr(_native, "WORKGROUP_FORM", int(group))
@@ -99,7 +99,7 @@ def test_ragged_windows_one_call_equal_separate_calls_and_oracle(beta, group, mo
     assert stats.density() == pytest.approx(float(np.mean(densities)), rel=1e-6)
 
 
-@pytest.mark.parametrize("group", ["1", "2", "3"])
+@pytest.mark.parametrize("group", ["1", "2"])
 def test_scatter_epilogue_equals_indexed_assignment(group, monkeypatch):
     monkeypatch.setattr(_native, "WORKGROUP_FORM", int(group))
     x, rows, keys = _ragged_case(12)

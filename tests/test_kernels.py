@@ -30,26 +30,27 @@ def kernel_pool(k, v, moments=True):
 
 
 def unswizzle(tiles):
-    """Tile pairs ``[B, H, N, 2, 64 D]`` -> K rows ``[B, H, N, 64, D]`` and
-    V^T rows ``[B, H, N, D, 64]`` (uint16 BF16 bits), undoing the bank swizzle."""
+    """Tile pairs ``[B, H, N, 2, 64 D]`` -> K and V rows ``[B, H, N, 64, D]``
+    (uint16 BF16 bits), undoing the tile layouts: K chunk c (8 features) of
+    row r sits at chunk c ^ (r & 15) (D = 128) or c ^ ((r >> 1) & 7) (D = 64)
+    of the row; V chunk c of row r at chunk (r >> 2) 4 CPR + (c >> 2) 16 +
+    (r & 3) 4 + (c & 3) of the tile (CPR = D / 8 chunks per row)."""
     t = tiles.cpu().view(torch.int16).numpy().view(np.uint16)
     b, h, n, _, e = t.shape
     d = e // 64
-    kt = t[:, :, :, 0].reshape(b, h, n, 64, d // 8, 8)
     rows = np.arange(64)[:, None]
     chunks = np.arange(d // 8)[None, :]
-    swz = (rows & 15) if d == 128 else ((rows >> 1) & 7)
-    k_rows = kt[:, :, :, rows, chunks ^ swz].reshape(b, h, n, 64, d)
-    vt = t[:, :, :, 1].reshape(b, h, n, d, 8, 2, 4)
-    dd = np.arange(d)[:, None]
-    g = np.arange(16)[None, :]                       # 4-key group g = keys 4g .. 4g + 3
-    chunk = (2 * (g >> 2) + (g & 1)) ^ ((dd & 7) ^ ((dd >> 3) & 1))
-    v_rows = vt[:, :, :, dd, chunk, (g >> 1) & 1].reshape(b, h, n, d, 64)
+    kswz = (rows & 15) if d == 128 else ((rows >> 1) & 7)
+    kt = t[:, :, :, 0].reshape(b, h, n, 64, d // 8, 8)
+    vt = t[:, :, :, 1].reshape(b, h, n, 64 * d // 8, 8)
+    k_rows = kt[:, :, :, rows, chunks ^ kswz].reshape(b, h, n, 64, d)
+    vpos = (rows >> 2) * (4 * (d // 8)) + (chunks >> 2) * 16 + (rows & 3) * 4 + (chunks & 3)
+    v_rows = vt[:, :, :, vpos].reshape(b, h, n, 64, d)
     return k_rows, v_rows
 
 
 def check_tiles(tiles, k, v):
-    """The attention tiles hold K / V^T of every key block, zero past the end."""
+    """The attention tiles hold K / V of every key block, zero past the end."""
     kb = k.contiguous().view(torch.int16).numpy().view(np.uint16)
     vb = v.contiguous().view(torch.int16).numpy().view(np.uint16)
     k_rows, v_rows = unswizzle(tiles)
@@ -58,15 +59,15 @@ def check_tiles(tiles, k, v):
     kp = np.concatenate([kb, np.zeros((b, pad) + kb.shape[2:], np.uint16)], 1)
     vp = np.concatenate([vb, np.zeros((b, pad) + vb.shape[2:], np.uint16)], 1)
     np.testing.assert_array_equal(k_rows, kp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 2, 4))
-    np.testing.assert_array_equal(v_rows, vp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 4, 2))
+    np.testing.assert_array_equal(v_rows, vp.reshape(b, nkb, 64, h, d).transpose(0, 3, 1, 2, 4))
 
 
 def centroids(ctiles, nkb):
     """Centroid tiles -> K and V block centroids ``[B, NKB, H, D]`` float32 (+ padding check)."""
-    k_rows, v_rows = unswizzle(ctiles)              # [B, H, NCT, 64, D], [B, H, NCT, D, 64]
+    k_rows, v_rows = unswizzle(ctiles)              # [B, H, NCT, 64, D] each
     b, h, nct, _, d = k_rows.shape
     kc = k_rows.reshape(b, h, nct * 64, d)
-    vc = v_rows.transpose(0, 1, 2, 4, 3).reshape(b, h, nct * 64, d)
+    vc = v_rows.reshape(b, h, nct * 64, d)
     assert (kc[:, :, nkb:] == 0).all() and (vc[:, :, nkb:] == 0).all()
     f = lambda x: orc.bf16_bits_to_f32(x[:, :, :nkb]).transpose(0, 2, 1, 3)
     return f(kc), f(vc)
@@ -84,7 +85,11 @@ def test_pooling_and_moments_bit_exact(shape):
     v = torch.randn(shape, generator=g, dtype=torch.bfloat16)
     out = kernel_pool(k.cuda(), v.cuda())
     torch.cuda.synchronize()
-    check_tiles(out["tiles"], k, v)
+    # Block tiles only where the attention kernels cannot read K / V rows
+    # themselves (fewer than 64 keys here).
+    assert (out["tiles"] is None) == (t >= 64)
+    if out["tiles"] is not None:
+        check_tiles(out["tiles"], k, v)
     kc = orc.block_means(to_np(k), True)          # [B, NKB, H, D]
     vc = orc.block_means(to_np(v), True)
     mean, var = orc.key_moments(kc)
@@ -191,7 +196,7 @@ def workload(name):
     return cfg, q, k, v
 
 
-@pytest.mark.parametrize("group", [1, 2, 3])
+@pytest.mark.parametrize("group", [1, 2])
 def test_c1_whole_call_against_oracle(group, monkeypatch):
     # B=1, T=1024, H=8, D=64, block-smooth (noise 0.1), seed 0, beta 1, sinks
     # 128, local 1: every query block of the call against the oracle.

@@ -33,24 +33,34 @@ def k8_rows(buf, d):
     return buf[rows[:, None], chunks].reshape(64, d)
 
 
-@pytest.mark.parametrize("d,nk", [(64, 317), (128, 317), (128, 64), (64, 1)])
+@pytest.mark.parametrize("d,nk", [(64, 317), (128, 317), (128, 64), (64, 1), (128, 65)])
 def test_quantised_key_tiles_equal_the_oracle(d, nk):
     q, k, v = tensors(nq=70, nk=nk, d=d, b=2, h=3, device="cuda", strided=True)
     k[0, :, 1] *= 40  # one head on a wider scale
     pooled = _native.pool_kv(k, v, moments=False, qk_int8=True)
     torch.cuda.synchronize()
+    shifted = pooled["tiles"] is None  # rows mode: the partial last block holds the last 64 keys
     b, h, nkb = pooled["k8_scale"].shape
     k8 = pooled["workspace"][pooled["k8_ptr"] - pooled["workspace"].data_ptr():][:b * h * nkb * 64 * d]
     k8 = k8.view(torch.int8).view(b, h, nkb, 64 * d).cpu().numpy()
-    ref_q, ref_s = orc.quantize_keys(k.float().cpu().numpy())
+    kf = k.float().cpu().numpy()
+    ref_q, ref_s = orc.quantize_keys(kf)
     np.testing.assert_array_equal(pooled["k8_scale"].cpu().numpy(), ref_s.transpose(0, 2, 1))
     for bi in range(b):
         for hi in range(h):
             for j in range(nkb):
                 rows = min(64, nk - 64 * j)
                 got = k8_rows(k8[bi, hi, j], d)
-                np.testing.assert_array_equal(got[:rows], ref_q[bi, 64 * j:64 * j + rows, hi])
-                assert (got[rows:] == 0).all()
+                if shifted and rows < 64:
+                    # Keys nk - 64 .. nk - 1: the block's own are the last `rows`;
+                    # the others (the previous block's) at this block's scale, clamped.
+                    np.testing.assert_array_equal(got[64 - rows:], ref_q[bi, 64 * j:, hi])
+                    inv = np.float32(127.0) / np.abs(kf[bi, 64 * j:, hi]).max()
+                    prev = np.clip(np.rint(kf[bi, nk - 64:64 * j, hi] * inv), -127, 127)
+                    np.testing.assert_array_equal(got[:64 - rows], prev)
+                else:
+                    np.testing.assert_array_equal(got[:rows], ref_q[bi, 64 * j:64 * j + rows, hi])
+                    assert (got[rows:] == 0).all()
 
 
 @pytest.mark.parametrize("group", ["1", "2"])
@@ -94,10 +104,7 @@ def test_int8_qk_indexed_windows():
     np.testing.assert_array_equal(stats.exact_blocks.cpu().numpy(), counts)
 
 
-def test_int8_qk_rejects_the_ping_pong_form_and_bad_names(monkeypatch):
+def test_int8_qk_rejects_unknown_precisions():
     q, k, v = tensors(device="cuda")
     with pytest.raises(ValueError):
         sol_attention(q, k, v, qk_precision="fp8")
-    monkeypatch.setattr(_native, "WORKGROUP_FORM", 3)
-    with pytest.raises(RuntimeError, match="forms 0, 1 and 2"):
-        sol_attention(q, k, v, qk_precision="int8")

@@ -38,9 +38,8 @@ def test_side_stream_matches_default_stream():
 
 def _capture_cases():
     """(name, setup(monkeypatch) -> call) for the launch shapes: the one-block
-    form; the two-block form and the ping-pong form with the pairing kernels
-    (dynamic-LDS lag kernel included); indexed windows with the fused scatter
-    into out=."""
+    form; the two-block form with the pairing kernels (dynamic-LDS lag kernel
+    included); indexed windows with the fused scatter into out=."""
 
     def plain(mp):
         q, k, v = inputs()
@@ -48,12 +47,6 @@ def _capture_cases():
 
     def paired(mp):
         mp.setattr(_native, "WORKGROUP_FORM", 2)
-        mp.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)
-        q, k, v = inputs()
-        return lambda: sol_attention(q, k, v, kv_sink_tokens=64)
-
-    def pingpong(mp):
-        mp.setattr(_native, "WORKGROUP_FORM", 3)
         mp.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)
         q, k, v = inputs()
         return lambda: sol_attention(q, k, v, kv_sink_tokens=64)
@@ -66,7 +59,7 @@ def _capture_cases():
         out = torch.zeros_like(q)
         return lambda: sol_attention_indexed(q, k, v, plan, beta=1.0, out=out)
 
-    return {"one-block": plain, "paired": paired, "ping-pong": pingpong, "indexed-scatter": indexed}
+    return {"one-block": plain, "paired": paired, "indexed-scatter": indexed}
 
 
 @pytest.mark.parametrize("case", sorted(_capture_cases()))

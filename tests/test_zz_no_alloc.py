@@ -31,10 +31,12 @@ def _noalloc(q, k, v, beta, local, kv_sink, q_sink, out, counts):
 
 
 # (batch, query tokens, key tokens, heads, head_dim, beta, local, kv sink, q sink);
-# the second case is smaller than the first, the third exercises beta = -inf.
+# the second case is smaller than the first, the third exercises beta = -inf,
+# the fourth fewer keys than one block (block tiles in the workspace).
 CASES = [(2, 4096, 4096, 16, 128, 1.0, 1, 128, 128),
          (1, 700, 1300, 3, 64, 0.5, 0, 64, 0),
-         (1, 500, 900, 2, 128, -math.inf, 1, 0, 0)]
+         (1, 500, 900, 2, 128, -math.inf, 1, 0, 0),
+         (1, 130, 40, 2, 64, 1.0, 1, 0, 0)]
 
 
 def test_noalloc_matches_the_allocating_path_on_consecutive_calls():
