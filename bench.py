@@ -397,7 +397,9 @@ def pool_bytes(b, tk, h, d, nkb, moments):
     """Algorithmic bytes of the pooling pass (read K and V once; write the K / V
     block centroids and, with moments, read them back for the mean and
     variance).  The query means are formed inside the attention kernel from
-    the Q tile it stages anyway, so pooling reads no Q."""
+    the Q tile it stages anyway, so pooling reads no Q.  BTHD keys are pooled
+    without any K / V tile copy: the attention kernels DMA the key rows
+    themselves, so these are all the bytes the pass moves."""
     reads = 2 * b * tk * h * d * 2
     writes = b * h * d * nkb * (2 + 2)
     return reads + writes + (b * nkb * h * d * 2 if moments else 0)
@@ -455,7 +457,6 @@ def measure(name, cfg, beta, args, dev, headline):
     exact_flops, approx_flops = routing_flops(dbg["selected"], tq, tk, d)
     attn_tflops = (exact_flops + approx_flops) / (attn_ms * 1e-3) / 1e12
     pbytes = pool_bytes(b, tk, h, d, nkb, finite)
-    relayout = 2 * b * h * nkb * 64 * d * 2  # the K / V^T tile copy the attention kernels stream
     traffic = measured_traffic(name)
     result = {
         "metric": METRIC,
@@ -486,9 +487,9 @@ def measure(name, cfg, beta, args, dev, headline):
                           "frac": pbytes / (pool_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                           "bytes_per_launch": pbytes,
                           "bytes_definition": "K and V read once + BF16 K/V centroids written"
-                                              + (" + centroids read for the moments" if finite else ""),
-                          "relayout_bytes_not_counted": relayout,
-                          "with_relayout_frac": (pbytes + relayout) / (pool_ms * 1e-3) / 1e9 / PEAK_HBM_GBS},
+                                              + (" + centroids read for the moments" if finite else "")
+                                              + "; no K/V tile copy (the attention kernels read K/V rows)",
+                          "kernels": "pool_kv_kernel + moments_kernel" if finite else "pool_kv_kernel"},
     }
     if headline and finite and not args.no_threshold_experiment:
         result["threshold_experiment"] = threshold_experiment(q, k, v, kw, out, density)

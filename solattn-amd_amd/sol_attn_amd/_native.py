@@ -328,7 +328,21 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
     per row, keys per block; the INT8-QK experiment).
     Returns ``(out, counts)`` (``counts`` None unless ``stats``) and, with
     ``debug=True``, a dict of routing diagnostics as a third element.
+
+    ``beta = -inf`` selects every key block: for plain BTHD inputs (no index,
+    protection, scatter or diagnostics) that is exact attention over all keys,
+    which the dense kernel computes with the same per-query tile order and
+    arithmetic (bit-identical output), without the pooling pass.  A forced
+    WORKGROUP_FORM keeps it on the SOL kernel.
     """
+    if (beta == -math.inf and WORKGROUP_FORM == 0 and rows is None and keys is None and protection is None
+            and key_lengths is None and out is None and not debug and qk_precision == "bf16"):
+        b, nq, h = q.shape[0], q.shape[1], q.shape[2]
+        dense = launch_dense(q, k, v, scale)
+        counts = None
+        if stats:
+            counts = torch.full((b, -(-nq // BLOCK), h), -(-k.shape[1] // BLOCK), device=q.device, dtype=torch.int32)
+        return dense, counts
     stream = _stream(q.device)
     pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths,
                      stream=stream, views=debug, qk_int8=qk_precision == "int8")

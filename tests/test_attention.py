@@ -63,6 +63,22 @@ def test_dense_strided_and_repeatable(d):
     assert torch.equal(actual, dense_attention(q, k, v))
 
 
+@pytest.mark.parametrize("shape", [(2, 193, 317, 2, 64), (1, 1025, 1089, 3, 128), (1, 70, 40, 2, 128)])
+def test_all_exact_beta_takes_the_dense_kernel_bit_identically(shape, monkeypatch):
+    # beta = -inf on plain inputs runs the dense kernel; the SOL kernel (a
+    # forced workgroup form) gives the same bits and exact-block counts.
+    b, nq, nk, h, d = shape
+    q, k, v = tensors(nq=nq, nk=nk, d=d, b=b, h=h, device="cuda", strided=True)
+    out, stats = sol_attention(q, k, v, beta=-math.inf, return_stats=True)
+    assert torch.equal(out, dense_attention(q, k, v))
+    for group in (1, 2):
+        monkeypatch.setattr(_native, "WORKGROUP_FORM", group)
+        sol, sol_stats = sol_attention(q, k, v, beta=-math.inf, return_stats=True)
+        assert torch.equal(out, sol)
+        assert torch.equal(stats.exact_blocks, sol_stats.exact_blocks)
+    assert stats.density() == 1.0
+
+
 def test_sol_zero_inputs_and_exact_sinks():
     # test_attention.py:83-93
     q, k, v = tensors(device="cuda")
