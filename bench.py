@@ -111,8 +111,11 @@ def make_inputs(cfg, device):
     return [q.to(device)[:, :, ::stride], k.to(device), v.to(device)]
 
 
-def event_ms(fn, reps):
-    """Average ms per call of fn() on the current stream (HIP events)."""
+def event_ms(fn, reps, warm=False):
+    """Average ms per call of fn() on the current stream (HIP events); `warm`
+    makes one untimed call first."""
+    if warm:
+        fn()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(reps):
@@ -357,9 +360,16 @@ def qk_int8_experiment(q, k, v, kw, cfg, bf16_out, bf16_counts, oracle_blocks):
             pooled = _native.pool_kv(k, v, moments=True, qk_int8=prec == "int8")
             attn_ms[prec] = event_ms(lambda: _native.attend(q, pooled, *args), 5)
             del pooled
+        # Every block exact, both on the SOL kernel (a forced workgroup form:
+        # plain BF16 calls with beta = -inf would take the dense kernel).
         every_block = dict(kw, beta=-math.inf)
-        all_exact_ms = {prec: event_ms(lambda: sol_attention(q, k, v, qk_precision=prec, **every_block), 3)
-                        for prec in ("bf16", "int8")}
+        form = _native.WORKGROUP_FORM
+        _native.WORKGROUP_FORM = 2
+        try:
+            all_exact_ms = {prec: event_ms(lambda: sol_attention(q, k, v, qk_precision=prec, **every_block), 3)
+                            for prec in ("bf16", "int8")}
+        finally:
+            _native.WORKGROUP_FORM = form
         quant_ms = event_ms(lambda: _native.pool_kv(k, v, moments=True, qk_int8=True), 5) - \
             event_ms(lambda: _native.pool_kv(k, v, moments=True), 5)
         control = dense_attention(q, k, v).float()
@@ -449,7 +459,10 @@ def measure(name, cfg, beta, args, dev, headline):
                                                   cfg["kv_sink_tokens"], cfg["query_sink_tokens"]), reps)
         ref_out, counts, dbg = _native.attend(q, pooled, scale, beta, cfg["local_blocks"],
                                               cfg["kv_sink_tokens"], cfg["query_sink_tokens"], debug=True)
-        dense_ms = event_ms(lambda: dense_attention(q, k, v), args.dense_reps)
+        # Small configurations: more repetitions and one warm call (their
+        # calls take tens of microseconds).
+        dense_ms = event_ms(lambda: dense_attention(q, k, v), args.dense_reps if headline else max(args.dense_reps, 20),
+                            warm=not headline)
     torch.cuda.synchronize()
     deterministic = bool(torch.equal(ref_out, out))
     nkb = dbg["selected"].shape[-1]
