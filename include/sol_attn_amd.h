@@ -43,7 +43,7 @@ extern "C" {
 
 #define SOL_ABI_VERSION 8
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
-#define SOL_MAX_KEY_BLOCKS 8192     /* routing bitmask capacity: key_tokens <= 524288 */
+#define SOL_MAX_KEY_TOKENS (1ll << 25) /* key_tokens of one pooling call (2^19 key blocks) */
 
 #define SOL_NOALLOC_SCRATCH_BYTES (128ll << 20) /* device workspace of sol_attention_noalloc */
 

@@ -57,13 +57,14 @@ def _validate(q, k, v, scale):
     return scale
 
 
-# Key blocks one call can route: the routing bitmask of each query block lives
-# in LDS (SOL_MAX_KEY_BLOCKS in include/sol_attn_amd.h).
-MAX_KEY_TOKENS = 8192 * 64
+# Key tokens one pooling call takes (SOL_MAX_KEY_TOKENS in
+# include/sol_attn_amd.h, 2^19 key blocks).  The attention kernel routes longer
+# key sequences in segments of 8,192 blocks, so this is the only bound.
+MAX_KEY_TOKENS = 1 << 25
 
 
 def _key_length(tokens):
-    """Rejects key sequences beyond the routing bitmask before any launch."""
+    """Rejects key sequences beyond the pooling bound before any launch."""
     if tokens > MAX_KEY_TOKENS:
         raise ValueError(f"Key sequences longer than {MAX_KEY_TOKENS} tokens are not supported")
 

@@ -402,9 +402,10 @@ __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next
 // more than count() times.
 template <int G>
 struct UnionCursor {
-  const uint32_t* mask;  // [G][stride] routing bitmasks
+  const uint32_t* mask;  // [G][stride] routing bitmasks of a key segment
   const uint32_t* mine;  // the calling wave's own row of mask
-  int stride, nkb;
+  int stride, nkb;       // mask row stride (words); the segment's key blocks
+  int base;              // the segment's first key block (bit i is block base + i)
   int word = -1;
   uint32_t bits = 0u, own = 0u;
 
@@ -432,7 +433,7 @@ struct UnionCursor {
     const int b = __builtin_ctz(bits);
     const int j = word * 32 + b;
     bits &= bits - 1u;
-    return j < nkb ? 2 * j + int((own >> b) & 1u) : 0;
+    return j < nkb ? 2 * (base + j) + int((own >> b) & 1u) : 0;
   }
 };
 
@@ -451,7 +452,7 @@ struct RangeCursor {
 // The bound names 256 threads for both workgroup forms, so the one-block form
 // (128 threads) is held to the same budget (with its own 128-thread bound the
 // compiler moves values through AGPRs instead).
-template <int D, int G, int R, bool Q8, bool KT>
+template <int D, int G, int R, bool Q8, bool KT, bool SEG>
 __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   using S = Shape<D>;
   using TL = TileLayout<D>;
@@ -482,7 +483,6 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   const bool live = qb < p.NQB;
   const int tk = batch_tokens(p.klen, b, p.Tk);  // this entry's key tokens
   const int nkb = (tk + kBlock - 1) / kBlock;      // its key blocks (<= p.NKB, the buffer stride)
-  const int nct = (nkb + kBlock - 1) / kBlock;     // its centroid tiles (<= p.NCT)
   const float scale_log2 = p.scale_log2;
 
   // 1. Q tiles -> LDS -> fragments.
@@ -594,126 +594,138 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
 
   State<D> st;
   state_init(st);
-  if (p.force == 1) {
-    // 3'. beta = -inf: every block exact, no centroid pass.
-    const int nwords = (nkb + 31) / 32;
-    for (int i = tid; i < G * nwords; i += NT) {
-      const int g = i / nwords, w = i % nwords;
-      const int nvalid = min(32, nkb - 32 * w);
-      s_mask[g][w] = slot_block(qb0 + g, p.NQB, stride) < p.NQB
-                         ? (nvalid == 32 ? ~0u : ((1u << nvalid) - 1u)) : 0u;
-    }
-    if (live && p.dbg_selected)
-      for (int j = lt; j < nkb; j += 128) p.dbg_selected[dbg_row + j] = 1;
-    __syncthreads();
-  } else {
-    // 3. Centroid pass.  Per tile: routing of the tile's 64 blocks for every
-    // query block of the group -- wave w scores blocks 32 (w & 1) + (lane & 31)
-    // of query block w >> 1 over feature half lane >> 5, the halves summed
-    // across the lane pair -- into the LDS bitmask; a barrier publishes the
-    // mask; then the approximated blocks' contributions.
-    const uint16_t* ctiles = p.ctiles + head * p.NCT * S::TILE;
-    auto process = [&](const uint16_t* buf, int ct, const auto& refill) {
-      const int r = fresh(32 * qh + col);  // centroid row inside the tile
-      const int j = kBlock * ct + r;
-      bool sel = false;
-      if (live && j < nkb) {
-        if (p.force == 0) {
-          const int c0 = fresh(hh) * (S::DC / 2);  // first 16-byte chunk of this lane's feature half
-          float part[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int c = 0; c < S::DC / 2; ++c) {
-            const int cc = c0 + c;
-            const u32x4 x = *reinterpret_cast<const u32x4*>(buf + TL::k_offset(r, cc));
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const uint32_t w = x[e >> 1];
-              part[e & 3] = fmaf(s_qm[qg][8 * cc + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)),
-                                 part[e & 3]);
-            }
-          }
-          const float proxy = pair_sum((part[0] + part[1]) + (part[2] + part[3]));
-          sel = proxy > s_cut[qg];
-          if (p.dbg_proxy && hh == 0) p.dbg_proxy[dbg_row + j] = proxy * p.scale;
-        }
-        sel = sel || (p.local_blocks >= 0 && abs(j - qb) <= p.local_blocks) || j < p.kv_sink_blocks ||
-              qb < p.q_sink_blocks;
-        if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * p.NKB + j] != 0;
-        if (p.dbg_selected && hh == 0) p.dbg_selected[dbg_row + j] = sel ? 1 : 0;
+  if (p.force == 1 && live && p.dbg_selected)
+    for (int j = lt; j < nkb; j += 128) p.dbg_selected[dbg_row + j] = 1;
+  int nsel = 0;  // this query block's selected blocks (kept by thread lt == 0)
+  // Stages 3 and 4 run once per segment of up to kMaxKeyBlocks key blocks
+  // (the LDS bitmask's capacity; segment s starts at block s kMaxKeyBlocks,
+  // which is centroid tile s kMaxKeyBlocks / 64), carrying one softmax
+  // state: the segment's centroid pass, then its exact pass.  SEG = false
+  // (key sequences of at most kMaxKeyBlocks blocks) compiles to one segment.
+  const int nseg = SEG ? (nkb + kMaxKeyBlocks - 1) / kMaxKeyBlocks : 1;
+  for (int si = 0; si < nseg; ++si) {
+    const int seg = si * kMaxKeyBlocks;                       // the segment's first key block
+    const int snkb = SEG ? min(kMaxKeyBlocks, nkb - seg) : nkb;  // its key blocks
+    const int ct0 = seg / kBlock;                             // its first centroid tile
+    if (seg > 0) lds_barrier();  // every wave is done with the last segment's mask and ring slots
+    if (p.force == 1) {
+      // 3'. beta = -inf: every block exact, no centroid pass.
+      const int nwords = (snkb + 31) / 32;
+      for (int i = tid; i < G * nwords; i += NT) {
+        const int g = i / nwords, w = i % nwords;
+        const int nvalid = min(32, snkb - 32 * w);
+        s_mask[g][w] = slot_block(qb0 + g, p.NQB, stride) < p.NQB
+                           ? (nvalid == 32 ? ~0u : ((1u << nvalid) - 1u)) : 0u;
       }
-      const uint64_t bal = __ballot(sel);
-      if (lane == 0) s_mask[qg][2 * ct + qh] = uint32_t(bal);
-      lds_barrier();  // publishes the mask words
-      // Branch-free: a tile with no approximated block for this query block
-      // (or a query block past the end) has every score at -inf and adds
-      // nothing.
-      const uint64_t approx = live ? tile_approx(s_mask[qg], ct, nkb) : 0ull;
-      centroid_tile<D>(st, buf, ct, approx, tk, qf, col, hh, scale_log2, refill);
-    };
-    auto always = [](int) { return true; };
-    tile_stream<D, NT, R>(ring, nct, RangeCursor{0},
-                          bf16_refills<D, NT>([=](int ct) { return ctiles + int64_t(ct) * S::TILE; }, wave, lane),
-                          tile_runs(always, process, process), process, wave, lane);
-    lds_barrier();  // every wave is done with the ring's centroid tiles
-  }
-  if (live && p.counts && lt == 0) {
-    int nsel = 0;
-    for (int w = 0; w < (nkb + 31) / 32; ++w) nsel += __builtin_popcount(s_mask[qg][w]);
-    p.counts[(int64_t(b) * p.NQB + qb) * p.H + h] = nsel;
-  }
+      __syncthreads();
+    } else {
+      // 3. Centroid pass.  Per tile: routing of the tile's 64 blocks for every
+      // query block of the group -- wave w scores blocks 32 (w & 1) + (lane & 31)
+      // of query block w >> 1 over feature half lane >> 5, the halves summed
+      // across the lane pair -- into the LDS bitmask (bit j - seg); a barrier
+      // publishes the mask; then the approximated blocks' contributions.
+      const uint16_t* ctiles = p.ctiles + head * p.NCT * S::TILE;
+      auto process = [&](const uint16_t* buf, int ct, const auto& refill) {
+        const int r = fresh(32 * qh + col);  // centroid row inside the tile
+        const int j = kBlock * ct + r;
+        bool sel = false;
+        if (live && j < nkb) {
+          if (p.force == 0) {
+            const int c0 = fresh(hh) * (S::DC / 2);  // first 16-byte chunk of this lane's feature half
+            float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < S::DC / 2; ++c) {
+              const int cc = c0 + c;
+              const u32x4 x = *reinterpret_cast<const u32x4*>(buf + TL::k_offset(r, cc));
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                const uint32_t w = x[e >> 1];
+                part[e & 3] = fmaf(s_qm[qg][8 * cc + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)),
+                                   part[e & 3]);
+              }
+            }
+            const float proxy = pair_sum((part[0] + part[1]) + (part[2] + part[3]));
+            sel = proxy > s_cut[qg];
+            if (p.dbg_proxy && hh == 0) p.dbg_proxy[dbg_row + j] = proxy * p.scale;
+          }
+          sel = sel || (p.local_blocks >= 0 && abs(j - qb) <= p.local_blocks) || j < p.kv_sink_blocks ||
+                qb < p.q_sink_blocks;
+          if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * p.NKB + j] != 0;
+          if (p.dbg_selected && hh == 0) p.dbg_selected[dbg_row + j] = sel ? 1 : 0;
+        }
+        const uint64_t bal = __ballot(sel);
+        if (lane == 0) s_mask[qg][2 * (ct - ct0) + qh] = uint32_t(bal);
+        lds_barrier();  // publishes the mask words
+        // Branch-free: a tile with no approximated block for this query block
+        // (or a query block past the end) has every score at -inf and adds
+        // nothing.
+        const uint64_t approx = live ? tile_approx(s_mask[qg], ct - ct0, snkb) : 0ull;
+        centroid_tile<D>(st, buf, ct, approx, tk, qf, col, hh, scale_log2, refill);
+      };
+      auto always = [](int) { return true; };
+      tile_stream<D, NT, R>(ring, (snkb + kBlock - 1) / kBlock, RangeCursor{ct0},
+                            bf16_refills<D, NT>([=](int ct) { return ctiles + int64_t(ct) * S::TILE; }, wave, lane),
+                            tile_runs(always, process, process), process, wave, lane);
+      lds_barrier();  // every wave is done with the ring's centroid tiles
+    }
+    if (live && p.counts && lt == 0)
+      for (int w = 0; w < (snkb + 31) / 32; ++w) nsel += __builtin_popcount(s_mask[qg][w]);
 
-  // 4. Exact pass over the union of the group's selected blocks.  Only the
-  // stream's last tile can be the partial tail block.
-  // Tile ids travel as tags 2 j + own-selection bit (UnionCursor).
-  UnionCursor<G> cursor{&s_mask[0][0], s_mask[qg], kMaskWords, nkb};
-  const int count = cursor.count();
-  const auto kv = kv_refills<D, NT, KT>(p, b, h, wave, lane);
-  auto selected = [](int tag) { return (tag & 1) != 0; };
-  auto miss = [&](const uint16_t*, int, const auto& refill) { refill.all(); };
-  if constexpr (!Q8) {
-    auto hit = [&](const uint16_t* buf, int, const auto& refill) {
-      full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
-    };
-    tile_stream<D, NT, R>(
-        ring, count, cursor, [=](int tag, uint32_t lds) { return kv(tag >> 1, lds); },
-        tile_runs(selected, hit, miss),
-        [&](const uint16_t* buf, int tag, const auto& refill) {
-          if (tag & 1) {
-            exact_tile<D, !KT>(st, buf, tag >> 1, tk, qf, col, hh, scale_log2, refill);
-          } else {
-            refill.all();
-          }
-        },
-        wave, lane);
-  } else {
-    // Quantised QK: INT8 K tiles and their scales (the V tiles as in the
-    // BF16 stream).
-    const int8_t* k8 = p.k8 + head * p.NKB * K8Layout<D>::kBytes;
-    const float* k8s = p.k8_scale + head * p.NKB;
-    auto make = [=](int tag, uint32_t lds) {
-      const int j = tag >> 1;
-      return Q8Refill<D, NT, decltype(kv(0, 0u))>(k8 + int64_t(j) * K8Layout<D>::kBytes, lds, wave, lane,
-                                                  kv(j, lds));
-    };
-    auto hit = [&](const uint16_t* buf, int tag, const auto& refill) {
-      tile_attend_i8<D, false>(st, buf, q8, col, hh, csq * k8s[tag >> 1], int2{}, refill);
-    };
-    tile_stream<D, NT, R>(
-        ring, count, cursor, make, tile_runs(selected, hit, miss),
-        [&](const uint16_t* buf, int tag, const auto& refill) {
-          if (tag & 1) {
-            const int j = tag >> 1;
-            const float c8 = csq * k8s[j];
-            if ((j + 1) * kBlock <= tk)
-              tile_attend_i8<D, false>(st, buf, q8, col, hh, c8, int2{}, refill);
-            else
-              tile_attend_i8<D, true>(st, buf, q8, col, hh, c8, tail_rows<!KT>(j, tk, hh), refill);
-          } else {
-            refill.all();
-          }
-        },
-        wave, lane);
-  }
+    // 4. Exact pass over the union of the group's selected blocks of the
+    // segment.  Only the last segment's last tile can be the partial tail
+    // block.  Tile ids travel as tags 2 j + own-selection bit (UnionCursor).
+    UnionCursor<G> cursor{&s_mask[0][0], s_mask[qg], kMaskWords, snkb, seg};
+    const int count = cursor.count();
+    const auto kv = kv_refills<D, NT, KT>(p, b, h, wave, lane);
+    auto selected = [](int tag) { return (tag & 1) != 0; };
+    auto miss = [&](const uint16_t*, int, const auto& refill) { refill.all(); };
+    if constexpr (!Q8) {
+      auto hit = [&](const uint16_t* buf, int, const auto& refill) {
+        full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
+      };
+      tile_stream<D, NT, R>(
+          ring, count, cursor, [=](int tag, uint32_t lds) { return kv(tag >> 1, lds); },
+          tile_runs(selected, hit, miss),
+          [&](const uint16_t* buf, int tag, const auto& refill) {
+            if (tag & 1) {
+              exact_tile<D, !KT>(st, buf, tag >> 1, tk, qf, col, hh, scale_log2, refill);
+            } else {
+              refill.all();
+            }
+          },
+          wave, lane);
+    } else {
+      // Quantised QK: INT8 K tiles and their scales (the V tiles as in the
+      // BF16 stream).
+      const int8_t* k8 = p.k8 + head * p.NKB * K8Layout<D>::kBytes;
+      const float* k8s = p.k8_scale + head * p.NKB;
+      auto make = [=](int tag, uint32_t lds) {
+        const int j = tag >> 1;
+        return Q8Refill<D, NT, decltype(kv(0, 0u))>(k8 + int64_t(j) * K8Layout<D>::kBytes, lds, wave, lane,
+                                                    kv(j, lds));
+      };
+      auto hit = [&](const uint16_t* buf, int tag, const auto& refill) {
+        tile_attend_i8<D, false>(st, buf, q8, col, hh, csq * k8s[tag >> 1], int2{}, refill);
+      };
+      tile_stream<D, NT, R>(
+          ring, count, cursor, make, tile_runs(selected, hit, miss),
+          [&](const uint16_t* buf, int tag, const auto& refill) {
+            if (tag & 1) {
+              const int j = tag >> 1;
+              const float c8 = csq * k8s[j];
+              if ((j + 1) * kBlock <= tk)
+                tile_attend_i8<D, false>(st, buf, q8, col, hh, c8, int2{}, refill);
+              else
+                tile_attend_i8<D, true>(st, buf, q8, col, hh, c8, tail_rows<!KT>(j, tk, hh), refill);
+            } else {
+              refill.all();
+            }
+          },
+          wave, lane);
+    }
+
+  }  // segments
+  if (live && p.counts && lt == 0) p.counts[(int64_t(b) * p.NQB + qb) * p.H + h] = nsel;
 
   // 5. Normalise and store.
   if (live) store_output<D>(p, b, h, qb * kBlock + myq, hh, st);
@@ -781,23 +793,36 @@ constexpr int kSolRing = 2;
 // one form (tests run both).
 constexpr int64_t kSmallLaunchGroups = 512;
 
-template <int D, int G>
-void launch_sol_group(const AttnParams& p, hipStream_t stream) {
+template <int D, int G, bool SEG>
+void launch_sol_variant(const AttnParams& p, hipStream_t stream) {
   // Grid of sol_task: the sink-holding tiles of every head, then xcd_task's.
   const int ntiles = (p.NQB + G - 1) / G, front = std::min(p.q_sink_blocks, ntiles);
   const unsigned grid = unsigned(front) * unsigned(p.B * p.H) + xcd_grid(p.B * p.H, ntiles - front);
   // Key blocks from pooled tile pairs (p.tiles) or straight from K / V rows.
   if (p.tiles) {
     if (p.k8)
-      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, true, true>), dim3(grid), dim3(128 * G), 0, stream, p);
+      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, true, true, SEG>), dim3(grid), dim3(128 * G), 0,
+                         stream, p);
     else
-      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, false, true>), dim3(grid), dim3(128 * G), 0, stream, p);
+      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, false, true, SEG>), dim3(grid), dim3(128 * G), 0,
+                         stream, p);
   } else {
     if (p.k8)
-      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, true, false>), dim3(grid), dim3(128 * G), 0, stream, p);
+      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, true, false, SEG>), dim3(grid), dim3(128 * G), 0,
+                         stream, p);
     else
-      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, false, false>), dim3(grid), dim3(128 * G), 0, stream, p);
+      hipLaunchKernelGGL((sol_attention_kernel<D, G, kSolRing, false, false, SEG>), dim3(grid), dim3(128 * G), 0,
+                         stream, p);
   }
+}
+
+template <int D, int G>
+void launch_sol_group(const AttnParams& p, hipStream_t stream) {
+  // Key sequences beyond one routing segment take the segmented kernel.
+  if (p.NKB > kMaxKeyBlocks)
+    launch_sol_variant<D, G, true>(p, stream);
+  else
+    launch_sol_variant<D, G, false>(p, stream);
 }
 
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {

@@ -157,7 +157,7 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
   if (moments && !(chunk_sums && key_mean && key_var && ctiles))
     return err(SOL_ERR_INVALID, "chunk_sums, key_mean and key_var go together (with ctiles)");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
-  if (nkb > (int64_t(1) << 19)) return err(SOL_ERR_UNSUPPORTED, "too many key blocks");
+  if (key_tokens > SOL_MAX_KEY_TOKENS) return err(SOL_ERR_UNSUPPORTED, "key_tokens exceeds SOL_MAX_KEY_TOKENS");
   sol::PoolParams p{};
   p.k = rows_of(k, k_strides, key_index, key_tokens, sequence_length);
   p.v = rows_of(v, v_strides, key_index, key_tokens, sequence_length);
@@ -260,8 +260,6 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
   if (!ctiles || !aligned16(ctiles) || !key_mean || !workspace || !key_cov)
     return fail(SOL_ERR_INVALID, "sol_key_covariance: ctiles (16-byte aligned), key_mean, workspace and key_cov are required");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
-  if (nkb > SOL_MAX_KEY_BLOCKS)
-    return fail(SOL_ERR_UNSUPPORTED, "sol_key_covariance: key_tokens exceeds 64 * SOL_MAX_KEY_BLOCKS");
   sol::CovParams p{};
   p.ctiles = static_cast<const uint16_t*>(ctiles);
   p.mean = key_mean;
@@ -315,8 +313,6 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
   const int64_t nqb = cdiv(query_tokens, SOL_BLOCK);
-  if (nkb > SOL_MAX_KEY_BLOCKS)
-    return fail(SOL_ERR_UNSUPPORTED, "sol_attention_fwd: key_tokens exceeds 64 * SOL_MAX_KEY_BLOCKS");
   if (batch * heads * nqb >= (int64_t(1) << 31))
     return fail(SOL_ERR_UNSUPPORTED, "sol_attention_fwd: grid too large");
   sol::AttnParams p;

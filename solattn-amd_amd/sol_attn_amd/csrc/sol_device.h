@@ -21,7 +21,7 @@ namespace sol {
 
 constexpr int kBlock = 64;      // tokens per physical block (kernels.py:12)
 constexpr int kWave = 64;       // CDNA wavefront width
-constexpr int kMaxKeyBlocks = 8192;  // LDS routing bitmask capacity (Tk <= 524288)
+constexpr int kMaxKeyBlocks = 8192;  // LDS routing bitmask capacity: key blocks routed per segment
 constexpr int kPoolChunk = 16;  // key blocks per pooling workgroup (= cascade chunk)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -119,7 +119,7 @@ def test_plan_records_whether_windows_share_rows():
 def test_key_length_cap_is_a_value_error():
     from sol_attn_amd import attention
     attention._key_length(attention.MAX_KEY_TOKENS)
-    with pytest.raises(ValueError, match="Key sequences longer than 524288 tokens"):
+    with pytest.raises(ValueError, match="Key sequences longer than 33554432 tokens"):
         attention._key_length(attention.MAX_KEY_TOKENS + 1)
 
 
