@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 8
+#define SOL_ABI_VERSION 9
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_TOKENS (1ll << 25) /* key_tokens of one pooling call (2^19 key blocks) */
 
@@ -130,6 +130,22 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
                        int64_t batch, int64_t key_tokens, int64_t heads, int64_t head_dim,
                        void* workspace, float* key_cov, void* stream);
 
+/* Bytes of the split_workspace sol_attention_fwd takes for a problem (0:
+ * the problem is not split, pass NULL).  Launches with at least two
+ * query-sink blocks and at most a quarter of the query blocks, at most
+ * 524,288 keys, and either fewer than 512 query-block pairs over all (entry,
+ * head) pairs (finite beta) or beta = +INFINITY and at most 8,192 query
+ * blocks, split the key blocks of sink blocks [0, 2 floor(sink blocks / 2))
+ * over up to 8 workgroups each (parts of at least 16 blocks); a merge kernel
+ * combines their partial softmax states.  Split launches pair adjacent query
+ * blocks (pair_strides is ignored).
+ * A sink block selects every key block, so without the split its workgroup
+ * ends long after the rest of a short launch.  The size is an upper bound
+ * for every workgroup_form.  No counterpart in the reference (one Triton
+ * program per query block). */
+int64_t sol_split_workspace_size(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                                 int64_t head_dim, double beta, int64_t query_sink_tokens);
+
 /* Fused routing + attention over the pooled keys of sol_pool_kv.
  * Replaces the `_threshold` and `_sol` launches of `launch_sol`
  * (kernels.py:203-225; kernels kernels.py:52-64 and 101-182).
@@ -142,6 +158,10 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
  * outward to whole blocks.  protection: NULL or uint8 [batch, NQB, NKB].
  * pair_strides: NULL (adjacent query blocks share a workgroup) or int32
  * [batch, heads] from sol_pair_strides (any value is a valid pairing).
+ * split_workspace: NULL (no split) or 16-byte aligned device memory of
+ * sol_split_workspace_size(batch, query_tokens, key_tokens, heads, head_dim,
+ * beta, query_sink_tokens) bytes when that is nonzero; split and unsplit
+ * calls agree to rounding (the parts' states merge in a fixed order).
  * out: contiguous BF16 [batch, query_tokens, heads, head_dim]; or, when
  * out_index (int64 [batch, query_tokens], device) is given, a contiguous BF16
  * [N, heads, head_dim] whose row out_index[b * query_tokens + t] receives
@@ -175,7 +195,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                       const void* tiles, const void* ctiles,
                       const float* key_mean, const float* key_var, const float* key_cov,
-                      const uint8_t* protection, const int32_t* pair_strides,
+                      const uint8_t* protection, const int32_t* pair_strides, void* split_workspace,
                       double scale, double beta, int64_t local_blocks,
                       int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
@@ -244,7 +264,8 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides,
  * whole 64-block tiles), and the moments; key blocks are read straight from K
  * and V (rows mode), except for fewer than 64 keys or token strides of 2^24
  * elements or more, where the block tiles (4 * head_dim bytes per key token
- * and head) join them.  Problems needing more than SOL_NOALLOC_SCRATCH_BYTES
+ * and head) join them, and the split workspace when the problem is split
+ * (sol_split_workspace_size).  Problems needing more than SOL_NOALLOC_SCRATCH_BYTES
  * (128 MiB) return SOL_ERR_UNSUPPORTED before any GPU work.  Every call on
  * one GPU shares that GPU's array: calls that overlap on one GPU (different
  * streams or threads) race and must be serialised by the caller. */

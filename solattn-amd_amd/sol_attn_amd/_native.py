@@ -16,7 +16,7 @@ import os
 import torch
 
 BLOCK = 64
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -36,9 +36,10 @@ _SIGNATURES = {
                      _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_pair_workspace_size": ([_i64, _i64, _i64, _i64], ctypes.c_int64),
     "sol_pair_strides": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "sol_split_workspace_size": ([_i64, _i64, _i64, _i64, _i64, _dbl, _i64], ctypes.c_int64),
     "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64,
                            _p, _i64p, _p, _i64p,
-                           _p, _p, _p, _p, _p, _p, _p,
+                           _p, _p, _p, _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
                            _p, _p, _p, _p, _p, _p, _p, _p, _int, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
@@ -259,6 +260,19 @@ def pair_strides(q, rows=None, min_blocks=None, stream=None):
     return strides
 
 
+# Split the query-sink tiles of short launches over several workgroups
+# (sol_split_workspace_size); False runs every tile in one workgroup.
+SPLIT_SINKS = True
+
+
+def split_workspace(b, nq, nk, h, d, beta, q_sink, device):
+    """The split workspace of an attention launch (None when it is not split)."""
+    if not SPLIT_SINKS:
+        return None
+    size = library().sol_split_workspace_size(b, nq, nk, h, d, float(beta), int(q_sink))
+    return torch.empty(size // 4, device=device, dtype=torch.float32) if size else None
+
+
 def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows=None,
            debug=False, out=None, stats=True, stream=None):
     """Routing + attention over pooled keys (the ``_sol`` launch of ``kernels.py:218-224``).
@@ -299,13 +313,14 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     if protection is not None:
         prot = protection.contiguous().view(torch.uint8)
     strides = pair_strides(q, rows, stream=stream) if PAIRING else None
+    split = split_workspace(b, nq, nk, h, d, beta, q_sink, dev)
     kr, vr = pooled["k"], pooled["v"]
     _check(lib.sol_attention_fwd(
         q.data_ptr(), _strides(q, indexed), _ptr(rows), q.shape[0] if indexed else 0,
         b, nq, nk, _ptr(pooled["key_lengths"]), h, d,
         _ptr(kr), None if kr is None else _strides(kr), _ptr(vr), None if vr is None else _strides(vr),
         pooled["tiles_ptr"], pooled["ctiles_ptr"], pooled["mean_ptr"], pooled["var_ptr"], pooled["cov_ptr"],
-        _ptr(prot), _ptr(strides), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
+        _ptr(prot), _ptr(strides), _ptr(split), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
         out.data_ptr(), _ptr(rows if scatter else None), _ptr(counts),
         _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
         pooled["k8_ptr"], pooled["k8_scale_ptr"], WORKGROUP_FORM, stream))

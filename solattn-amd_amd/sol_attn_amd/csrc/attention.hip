@@ -394,17 +394,19 @@ __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next
 }
 
 // Exact tiles of a SOL workgroup: the union of its G query blocks' selected
-// blocks, ascending, as tags 2 j + (whether the calling wave's own query
-// block selected j), so that the stream needs no LDS read per tile to tell
-// the wave's tiles from its partners'.  The exact phase starts (word 0
-// loaded) on the first call; the word scan never passes the last mask word
-// and every id is below nkb, so the cursor yields valid tiles even if called
-// more than count() times.
+// blocks among bits [lo, hi) of a segment's masks, ascending, as tags
+// 2 j + (whether the calling wave's own query block selected j), so that the
+// stream needs no LDS read per tile to tell the wave's tiles from its
+// partners'.  Only mask words overlapping [lo, hi) are read, and only their
+// bits inside it.  The exact phase starts (word lo / 32 loaded) on the first
+// call; the word scan never passes the range's last word, so the cursor
+// yields valid tiles even if called more than count() times.
 template <int G>
 struct UnionCursor {
   const uint32_t* mask;  // [G][stride] routing bitmasks of a key segment
   const uint32_t* mine;  // the calling wave's own row of mask
-  int stride, nkb;       // mask row stride (words); the segment's key blocks
+  int stride;            // mask row stride (words)
+  int lo, hi;            // the streamed bits of the segment's masks
   int base;              // the segment's first key block (bit i is block base + i)
   int word = -1;
   uint32_t bits = 0u, own = 0u;
@@ -413,11 +415,11 @@ struct UnionCursor {
     uint32_t u = 0;
 #pragma unroll
     for (int g = 0; g < G; ++g) u |= mask[g * stride + w];
-    return u;
+    return u & uint32_t(bit_range64(lo - 32 * w, hi - 32 * w));
   }
   __device__ __forceinline__ int count() const {
     int n = 0;
-    for (int w = 0; w < (nkb + 31) / 32; ++w) n += __builtin_popcount(union_word(w));
+    for (int w = lo / 32; w < (hi + 31) / 32; ++w) n += __builtin_popcount(union_word(w));
     return n;
   }
   __device__ __forceinline__ void load(int w) {
@@ -426,14 +428,14 @@ struct UnionCursor {
     own = uint32_t(__builtin_amdgcn_readfirstlane(mine[w]));  // wave-uniform: the wave's own row
   }
   __device__ __forceinline__ int operator()() {
-    const int last = (nkb + 31) / 32 - 1;
-    if (word < 0) load(0);
+    const int last = (hi + 31) / 32 - 1;
+    if (word < 0) load(lo / 32);
     while (bits == 0 && word < last) load(word + 1);
-    if (bits == 0) return 0;  // unreachable when called count() times
+    if (bits == 0) return 2 * (base + lo);  // unreachable when called count() times
     const int b = __builtin_ctz(bits);
-    const int j = word * 32 + b;
+    const int j = word * 32 + b;  // < hi: union_word keeps only bits inside the range
     bits &= bits - 1u;
-    return j < nkb ? 2 * (base + j) + int((own >> b) & 1u) : 0;
+    return 2 * (base + j) + int((own >> b) & 1u);
   }
 };
 
@@ -466,7 +468,9 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   __shared__ uint32_t s_mask[G][kMaskWords];
 
   const int ntiles = (p.NQB + G - 1) / G;
-  const TileTask task = sol_task(blockIdx.x, ntiles, min(p.q_sink_blocks, ntiles), p.B * p.H);
+  const int front = min(p.q_sink_blocks, ntiles);
+  const int split_tiles = sink_split_tiles(p.splits, p.q_sink_blocks, G, front);
+  const TileTask task = sol_task(blockIdx.x, ntiles, front, split_tiles, p.B * p.H, p.splits);
   if (task.bh < 0) return;
   const int bh = task.bh;
   const int h = bh % p.H, b = bh / p.H;
@@ -478,11 +482,15 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   const int lt = tid & 127;                  // thread index inside the query block's 2 waves
   const int qb0 = task.tile * G;  // first slot of this group
   // Query-block pairing stride (any value is a valid pairing; see slot_block).
-  const int stride = p.pair_stride ? min(p.pair_stride[bh], p.NQB) : 0;
+  const int stride = p.pair_stride && p.splits == 1 ? min(p.pair_stride[bh], p.NQB) : 0;
   const int qb = slot_block(qb0 + qg, p.NQB, stride);
   const bool live = qb < p.NQB;
   const int tk = batch_tokens(p.klen, b, p.Tk);  // this entry's key tokens
   const int nkb = (tk + kBlock - 1) / kBlock;      // its key blocks (<= p.NKB, the buffer stride)
+  // A split front tile's workgroup routes and attends key blocks [range.x,
+  // range.y) only and leaves its partial state to sol_merge_kernel.
+  const int nsplit = task.tile < split_tiles ? p.splits : 1;
+  const int2 range = split_range(task.split, nsplit, nkb);
   const float scale_log2 = p.scale_log2;
 
   // 1. Q tiles -> LDS -> fragments.
@@ -588,7 +596,7 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   }
   __syncthreads();  // cutoffs published; Q staging is dead and the ring is free
   const int64_t dbg_row = ((int64_t(b) * p.NQB + qb) * p.H + h) * p.NKB;
-  if (live && p.dbg_cutoff && lt == 0)
+  if (live && p.dbg_cutoff && lt == 0 && task.split == 0)
     p.dbg_cutoff[(int64_t(b) * p.NQB + qb) * p.H + h] =
         p.force == 0 ? s_cut[qg] * p.scale : (p.force == 1 ? kNegInf : -kNegInf);
 
@@ -607,6 +615,8 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
     const int seg = si * kMaxKeyBlocks;                       // the segment's first key block
     const int snkb = SEG ? min(kMaxKeyBlocks, nkb - seg) : nkb;  // its key blocks
     const int ct0 = seg / kBlock;                             // its first centroid tile
+    // This workgroup's blocks of the segment, as bits of its masks.
+    const int r0 = max(seg, range.x) - seg, r1 = min(seg + snkb, range.y) - seg;
     if (seg > 0) lds_barrier();  // every wave is done with the last segment's mask and ring slots
     if (p.force == 1) {
       // 3'. beta = -inf: every block exact, no centroid pass.
@@ -629,7 +639,7 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
         const int r = fresh(32 * qh + col);  // centroid row inside the tile
         const int j = kBlock * ct + r;
         bool sel = false;
-        if (live && j < nkb) {
+        if (live && j >= seg + r0 && j < seg + r1) {
           if (p.force == 0) {
             const int c0 = fresh(hh) * (S::DC / 2);  // first 16-byte chunk of this lane's feature half
             float part[4] = {0.f, 0.f, 0.f, 0.f};
@@ -659,22 +669,25 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
         // Branch-free: a tile with no approximated block for this query block
         // (or a query block past the end) has every score at -inf and adds
         // nothing.
-        const uint64_t approx = live ? tile_approx(s_mask[qg], ct - ct0, snkb) : 0ull;
+        const uint64_t approx = live ? tile_approx(s_mask[qg], ct - ct0, r0, r1) : 0ull;
         centroid_tile<D>(st, buf, ct, approx, tk, qf, col, hh, scale_log2, refill);
       };
       auto always = [](int) { return true; };
-      tile_stream<D, NT, R>(ring, (snkb + kBlock - 1) / kBlock, RangeCursor{ct0},
+      const int ct_lo = ct0 + r0 / kBlock;  // the centroid tiles holding blocks [r0, r1)
+      const int nct = r1 > r0 ? ct0 + (r1 - 1) / kBlock - ct_lo + 1 : 0;
+      tile_stream<D, NT, R>(ring, nct, RangeCursor{ct_lo},
                             bf16_refills<D, NT>([=](int ct) { return ctiles + int64_t(ct) * S::TILE; }, wave, lane),
                             tile_runs(always, process, process), process, wave, lane);
       lds_barrier();  // every wave is done with the ring's centroid tiles
     }
     if (live && p.counts && lt == 0)
-      for (int w = 0; w < (snkb + 31) / 32; ++w) nsel += __builtin_popcount(s_mask[qg][w]);
+      for (int w = r0 / 32; w < (r1 + 31) / 32; ++w)
+        nsel += __builtin_popcount(s_mask[qg][w] & uint32_t(bit_range64(r0 - 32 * w, r1 - 32 * w)));
 
     // 4. Exact pass over the union of the group's selected blocks of the
     // segment.  Only the last segment's last tile can be the partial tail
     // block.  Tile ids travel as tags 2 j + own-selection bit (UnionCursor).
-    UnionCursor<G> cursor{&s_mask[0][0], s_mask[qg], kMaskWords, snkb, seg};
+    UnionCursor<G> cursor{&s_mask[0][0], s_mask[qg], kMaskWords, r0, r1, seg};
     const int count = cursor.count();
     const auto kv = kv_refills<D, NT, KT>(p, b, h, wave, lane);
     auto selected = [](int tag) { return (tag & 1) != 0; };
@@ -725,6 +738,33 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
     }
 
   }  // segments
+  if (nsplit > 1) {
+    // Partial state of this key range: the record of row (tile, part,
+    // query) holds acc (features in output order), m, the pair-summed
+    // denominator and the query block's count of selected blocks.
+    const float den = pair_sum(st.den);
+    float* rec = p.partial +
+                 (((int64_t(bh) * split_tiles + task.tile) * nsplit + task.split) * (G * kBlock) + qg * kBlock + myq) *
+                     kPartialRow<D>;
+#pragma unroll
+    for (int dt = 0; dt < S::DT; ++dt)
+#pragma unroll
+      for (int k4 = 0; k4 < 4; ++k4) {
+        f32x4 x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = st.acc[dt][4 * k4 + i];
+        *reinterpret_cast<f32x4*>(rec + dt * 32 + 8 * k4 + 4 * hh) = x;
+      }
+    if (hh == 0) {
+      f32x4 x;
+      x[0] = st.m;
+      x[1] = den;
+      x[2] = float(nsel);  // thread lt == 0's (the query block's first row)
+      x[3] = 0.f;
+      *reinterpret_cast<f32x4*>(rec + D) = x;
+    }
+    return;
+  }
   if (live && p.counts && lt == 0) p.counts[(int64_t(b) * p.NQB + qb) * p.H + h] = nsel;
 
   // 5. Normalise and store.
@@ -783,6 +823,61 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   store_output<D>(p, b, h, q0 + myq, hh, st);
 }
 
+// Combines the partial states of split sink tiles (sol_task): per query
+// row, m = max_s m_s, O = sum_s 2^(m_s - m) acc_s / sum_s 2^(m_s - m) den_s
+// over the parts in ascending order; stores O as store_output does, and the
+// query block's count (the parts' counts summed).  One thread per row and 4
+// features; rows [B H][split_tiles][G 64] (adjacent pairing: tile t holds
+// query blocks G t ..).
+constexpr int kMergeThreads = 256;
+
+template <int D, int G>
+__global__ __launch_bounds__(kMergeThreads) void sol_merge_kernel(AttnParams p, int split_tiles) {
+  constexpr int kChunks = D / 4;
+  constexpr int kRows = kMergeThreads / kChunks;
+  constexpr int RW = kPartialRow<D>;
+  constexpr int kTileRows = G * kBlock;
+  const int nsplit = p.splits;
+  const int64_t row = int64_t(blockIdx.x) * kRows + threadIdx.x / kChunks;
+  const int c = threadIdx.x % kChunks;
+  if (row >= int64_t(p.B) * p.H * split_tiles * kTileRows) return;
+  const int r = int(row % kTileRows);   // qg 64 + query
+  const int64_t bt = row / kTileRows;   // bh split_tiles + tile
+  const int tile = int(bt % split_tiles), bh = int(bt / split_tiles);
+  const int h = bh % p.H, b = bh / p.H;
+  const int qb = tile * G + r / kBlock;
+  if (qb >= p.NQB) return;
+  const float* rec0 = p.partial + (bt * nsplit * kTileRows + r) * RW;
+  const int64_t part = int64_t(kTileRows) * RW;  // floats between one row's parts
+  float m = kNegInf;
+  for (int s = 0; s < nsplit; ++s) m = fmaxf(m, rec0[s * part + D]);
+  float den = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  int count = 0;
+  for (int s = 0; s < nsplit; ++s) {
+    const float* rec = rec0 + s * part;
+    const f32x4 tail = *reinterpret_cast<const f32x4*>(rec + D);  // m, den, count
+    const float w = tail[0] == kNegInf ? 0.f : fast_exp2(tail[0] - m);
+    den = den + w * tail[1];
+    count += int(tail[2]);
+    const f32x4 x = *reinterpret_cast<const f32x4*>(rec + 4 * c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = o[i] + w * x[i];
+  }
+  const int t = qb * kBlock + r % kBlock;
+  if (p.counts && r % kBlock == 0 && c == 0) p.counts[(int64_t(b) * p.NQB + qb) * p.H + h] = count;
+  if (t >= p.Tq) return;
+  int64_t orow = int64_t(b) * p.Tq + t;
+  if (p.out_index) {
+    orow = p.out_index[orow];
+    if (orow < 0 || orow >= p.out_rows) return;  // outside the output: not stored
+  }
+  u32x2 v;
+  v[0] = pack_bf16x2(__fdiv_rn(o[0], den), __fdiv_rn(o[1], den));
+  v[1] = pack_bf16x2(__fdiv_rn(o[2], den), __fdiv_rn(o[3], den));
+  *reinterpret_cast<u32x2*>(p.out + (orow * p.H + h) * D + 4 * c) = v;
+}
+
 // LDS ring depth of the SOL kernel.
 constexpr int kSolRing = 2;
 // Below this many two-block workgroups the launch leaves CUs idle (256 CUs x
@@ -795,9 +890,12 @@ constexpr int64_t kSmallLaunchGroups = 512;
 
 template <int D, int G, bool SEG>
 void launch_sol_variant(const AttnParams& p, hipStream_t stream) {
-  // Grid of sol_task: the sink-holding tiles of every head, then xcd_task's.
+  // Grid of sol_task: the sink-holding tiles of every head (p.splits
+  // workgroups each), then xcd_task's.
   const int ntiles = (p.NQB + G - 1) / G, front = std::min(p.q_sink_blocks, ntiles);
-  const unsigned grid = unsigned(front) * unsigned(p.B * p.H) + xcd_grid(p.B * p.H, ntiles - front);
+  const int split_tiles = sink_split_tiles(p.splits, p.q_sink_blocks, G, front);
+  const unsigned grid = unsigned(split_tiles * (p.splits - 1) + front) * unsigned(p.B * p.H) +
+                        xcd_grid(p.B * p.H, ntiles - front);
   // Key blocks from pooled tile pairs (p.tiles) or straight from K / V rows.
   if (p.tiles) {
     if (p.k8)
@@ -823,6 +921,14 @@ void launch_sol_group(const AttnParams& p, hipStream_t stream) {
     launch_sol_variant<D, G, true>(p, stream);
   else
     launch_sol_variant<D, G, false>(p, stream);
+  const int front = std::min(p.q_sink_blocks, (p.NQB + G - 1) / G);
+  const int split_tiles = sink_split_tiles(p.splits, p.q_sink_blocks, G, front);
+  if (split_tiles > 0) {
+    constexpr int kRows = kMergeThreads / (D / 4);
+    const int64_t rows = int64_t(p.B) * p.H * split_tiles * G * kBlock;
+    hipLaunchKernelGGL((sol_merge_kernel<D, G>), dim3(unsigned((rows + kRows - 1) / kRows)), dim3(kMergeThreads), 0,
+                       stream, p, split_tiles);
+  }
 }
 
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {

@@ -24,6 +24,7 @@ constexpr int kXcds = 8;
 // a slice return -1 (idle workgroup).
 struct TileTask {
   int bh, tile;
+  int split = 0;  // key-range part of a split front tile (sol_task)
 };
 
 __device__ __forceinline__ TileTask xcd_task(int i, int ntiles) {
@@ -38,14 +39,39 @@ __device__ __forceinline__ TileTask xcd_task(int i, int ntiles) {
 // sink query blocks, whose workgroups stream every key block and run several
 // times longer than the others; in xcd_task order the last heads' ones would
 // start late and set the kernel's end (2 x 4,096 tokens x 16 heads with
-// 128-token sinks: 251 -> 163 us).  The remaining tiles keep the xcd_task map.
-__device__ __forceinline__ TileTask sol_task(int i, int ntiles, int front, int heads) {
-  const int nfront = front * heads;
-  if (i < nfront) return TileTask{i % heads, i / heads};
+// 128-token sinks: 251 -> 163 us).  The first `split_tiles` of them (<=
+// front) are `splits` workgroups each, one per key range (split_range), whose
+// partial states sol_merge_kernel combines.  The remaining tiles keep the
+// xcd_task map.
+__device__ __forceinline__ TileTask sol_task(int i, int ntiles, int front, int split_tiles, int heads,
+                                             int splits) {
+  const int nsplit = split_tiles * heads * splits;
+  if (i < nsplit) {
+    const int j = i / heads;
+    return TileTask{i % heads, j / splits, j % splits};
+  }
+  i -= nsplit;
+  const int nrest = (front - split_tiles) * heads;
+  if (i < nrest) return TileTask{i % heads, split_tiles + i / heads};
   if (ntiles <= front) return TileTask{-1, 0};
-  TileTask t = xcd_task(i - nfront, ntiles - front);
+  TileTask t = xcd_task(i - nrest, ntiles - front);
   t.tile += front;
   return t;
+}
+
+// Query-sink tiles split by key range (sol_task) when a launch is split: the
+// tiles of sink blocks [0, 2 floor(q_sink_blocks / 2)).  With adjacent
+// pairing those tiles hold sink blocks only, in either workgroup form, so
+// whether a query block is split depends on its index alone and both forms
+// stay bit-identical.  A split launch pairs adjacent blocks (it ignores
+// pair_stride).
+__host__ __device__ inline int sink_split_tiles(int splits, int q_sink_blocks, int G, int front) {
+  return splits > 1 ? min(front, (q_sink_blocks / 2 * 2) / G) : 0;
+}
+
+// Key blocks [lo, hi) of part s of n of a key sequence of nkb blocks.
+__device__ __forceinline__ int2 split_range(int s, int n, int nkb) {
+  return int2{int(int64_t(s) * nkb / n), int(int64_t(s + 1) * nkb / n)};
 }
 
 __host__ __device__ inline unsigned xcd_grid(int heads, int ntiles) {
@@ -68,6 +94,11 @@ struct State {
   float m;                   // running max, log2 units (-inf: nothing yet)
   float den;                 // partial denominator over this lane's key rows
 };
+
+// Floats per query row of a split workgroup's partial state: acc (D), m,
+// den, count, padding (sol_attention_kernel, sol_merge_kernel).
+template <int D>
+constexpr int kPartialRow = D + 4;
 
 template <int D>
 __device__ __forceinline__ void state_init(State<D>& st) {
@@ -494,11 +525,19 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Approximated blocks of centroid tile ct for one query block: valid blocks
-// whose routing bit is clear.
-__device__ __forceinline__ uint64_t tile_approx(const uint32_t* mask, int ct, int nkb) {
-  const int nvalid = min(64, nkb - 64 * ct);
-  const uint64_t valid = nvalid == 64 ? ~0ull : ((1ull << nvalid) - 1ull);
+// Bits i of a 64-bit word with lo <= i < hi (any lo, hi).
+__device__ __forceinline__ uint64_t bit_range64(int lo, int hi) {
+  lo = max(lo, 0);
+  hi = min(hi, 64);
+  if (hi <= lo) return 0ull;
+  const uint64_t upto = hi == 64 ? ~0ull : ((1ull << hi) - 1ull);
+  return upto & ~((1ull << lo) - 1ull);
+}
+
+// Approximated blocks of centroid tile ct for one query block: blocks of the
+// range [lo, hi) whose routing bit is clear.
+__device__ __forceinline__ uint64_t tile_approx(const uint32_t* mask, int ct, int lo, int hi) {
+  const uint64_t valid = bit_range64(lo - 64 * ct, hi - 64 * ct);
   const uint64_t sel = uint64_t(mask[2 * ct]) | (uint64_t(mask[2 * ct + 1]) << 32);
   return valid & ~sel;
 }

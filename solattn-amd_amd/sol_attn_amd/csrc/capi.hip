@@ -86,6 +86,43 @@ int scratch_on_current_device(void** ptr) {
 
 int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
+// Key-range parts per query-sink tile of the SOL kernel (sol_task).  A
+// query-sink block selects every key block, so its workgroup streams all of
+// them and, in a launch of few workgroups, ends long after the rest.  Split:
+// launches of one-block workgroups (fewer than 512 query-block pairs over all
+// (entry, head) pairs, the default schedule's threshold) at finite beta, and
+// at beta = +inf (every other workgroup streams its protected blocks only)
+// launches of up to 8,192 query blocks (8 rounds of 512 two-block
+// workgroups).  Parts hold at least 16 key blocks, at most 8 parts, while
+// their partial states fit kSplitBytesMax.  Measured (us per call, 4 heads,
+// beta 1): 4,096 tokens 97 -> 60, 8,192 tokens 172 -> 108; at 2 x 4,096 x 16
+// heads beta +inf 109 -> 91, while beta 0 or 1 there gains nothing (the
+// launch is bound by its two rounds of workgroups, and the extra
+// workgroups and the merge cost 1-4%).  beta = -inf (every block exact),
+// fewer than two sink blocks and sinks over a quarter of the query blocks
+// are not split.
+constexpr int64_t kSplitBytesMax = int64_t(64) << 20;
+
+int64_t split_bytes(int64_t bh, int64_t q_sink_blocks, int64_t splits, int64_t head_dim) {
+  // Split tiles hold sink blocks [0, 2 floor(q_sink_blocks / 2)) (sink_split_tiles).
+  return splits > 1 ? bh * (q_sink_blocks / 2 * 2) * SOL_BLOCK * splits * (head_dim + 4) * 4 : 0;
+}
+
+int sink_splits(int64_t bh, int64_t nqb, int64_t nkb, int64_t q_sink_blocks, int force, int64_t head_dim) {
+  const bool one_block_groups = bh * ((nqb + 1) / 2) < 512;
+  if (force == 1 || q_sink_blocks < 2 || 4 * q_sink_blocks > nqb || nkb > sol::kMaxKeyBlocks ||
+      !(one_block_groups || (force == 2 && bh * nqb <= 8192)))
+    return 1;
+  int64_t s = std::min<int64_t>(8, nkb / 16);
+  while (s > 1 && split_bytes(bh, q_sink_blocks, s, head_dim) > kSplitBytesMax) --s;
+  return int(std::max<int64_t>(s, 1));
+}
+
+int64_t sink_blocks(int64_t query_sink_tokens) {
+  const int64_t big = int64_t(1) << 30;
+  return cdiv(query_sink_tokens > big ? big : query_sink_tokens, SOL_BLOCK);
+}
+
 // Attention kernels DMA key blocks straight from K / V rows ("rows mode",
 // no pooled tiles) when the keys are plain strided rows of equal length, at
 // least one block of them, with row strides whose 64-row spans fit the
@@ -273,6 +310,17 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
   return hip_status(sol::launch_covariance(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
+int64_t sol_split_workspace_size(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                                 int64_t head_dim, double beta, int64_t query_sink_tokens) {
+  if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 || key_tokens >= (int64_t(1) << 30) ||
+      query_sink_tokens < 0 || std::isnan(beta))
+    return 0;
+  const int64_t bh = batch * heads, nqb = cdiv(query_tokens, SOL_BLOCK), qsb = sink_blocks(query_sink_tokens);
+  const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
+  const int s = sink_splits(bh, nqb, cdiv(key_tokens, SOL_BLOCK), qsb, force, head_dim);
+  return split_bytes(bh, qsb, s, head_dim);
+}
+
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t sequence_length, int64_t batch, int64_t query_tokens,
                       int64_t key_tokens,
@@ -280,7 +328,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                       const void* tiles, const void* ctiles, const float* key_mean,
                       const float* key_var, const float* key_cov, const uint8_t* protection,
-                      const int32_t* pair_strides, double scale, double beta,
+                      const int32_t* pair_strides, void* split_workspace, double scale, double beta,
                       int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
@@ -303,8 +351,10 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   if (kv_sink_tokens < 0 || query_sink_tokens < 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: sink token counts must be nonnegative");
   const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
-  if (!ctiles || !aligned16(ctiles) || !out || !aligned16(out) || (tiles && !aligned16(tiles)))
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: tiles/ctiles/out must be 16-byte aligned device buffers");
+  if (!ctiles || !aligned16(ctiles) || !out || !aligned16(out) || (tiles && !aligned16(tiles)) ||
+      (split_workspace && !aligned16(split_workspace)))
+    return fail(SOL_ERR_INVALID,
+                "sol_attention_fwd: tiles/ctiles/out/split_workspace must be 16-byte aligned device buffers");
   if (!tiles) {
     const int rc = rows_mode_ok("sol_attention_fwd", k, k_strides, v, v_strides, key_lengths, key_tokens);
     if (rc != SOL_OK) return rc;
@@ -354,7 +404,9 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   const int64_t big = int64_t(1) << 30;
   p.local_blocks = int(local_blocks < 0 ? -1 : (local_blocks > big ? big : local_blocks));
   p.kv_sink_blocks = int(cdiv(kv_sink_tokens > big ? big : kv_sink_tokens, SOL_BLOCK));
-  p.q_sink_blocks = int(cdiv(query_sink_tokens > big ? big : query_sink_tokens, SOL_BLOCK));
+  p.q_sink_blocks = int(sink_blocks(query_sink_tokens));
+  p.splits = split_workspace ? sink_splits(batch * heads, nqb, nkb, p.q_sink_blocks, force, head_dim) : 1;
+  p.partial = p.splits > 1 ? static_cast<float*>(split_workspace) : nullptr;
   return hip_status(sol::launch_sol(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
@@ -454,7 +506,10 @@ int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k
   const int64_t off_sums = off_tiles + (rows ? 0 : align256(sizes[1]));
   const int64_t off_mean = off_sums + align256(sizes[2]);
   const int64_t off_var = off_mean + align256(sizes[3]);
-  const int64_t need = moments ? off_var + align256(sizes[3]) : off_sums;
+  const int64_t off_split = moments ? off_var + align256(sizes[3]) : off_sums;
+  const int64_t split = sol_split_workspace_size(batch, query_tokens, key_tokens, heads, head_dim, beta,
+                                                 query_sink_tokens);
+  const int64_t need = off_split + align256(split);
   if (need > SOL_NOALLOC_SCRATCH_BYTES)
     return fail(SOL_ERR_UNSUPPORTED,
                 "sol_attention_noalloc: the pooled keys need more than SOL_NOALLOC_SCRATCH_BYTES "
@@ -472,7 +527,7 @@ int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k
   if (prc != SOL_OK) return prc;
   return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
                            head_dim, k, k_strides, v, v_strides, tiles, ws, mean, var, nullptr, nullptr, nullptr,
-                           scale, beta,
+                           split ? ws + off_split : nullptr, scale, beta,
                            local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr, counts, nullptr,
                            nullptr, nullptr, nullptr, nullptr, 0, stream);
 }

@@ -41,6 +41,7 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 }
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 // Two floats -> two round-to-nearest-even bf16 in one v_cvt_pk_bf16_f32

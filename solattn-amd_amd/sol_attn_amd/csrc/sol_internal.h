@@ -80,6 +80,8 @@ struct AttnParams {
   int kv_sink_blocks, q_sink_blocks;
   int workgroup_form;  // 0: by launch size; 1 / 2: query blocks per workgroup of
                        // sol_attention_kernel
+  int splits;          // key-range parts per front (query-sink) tile, >= 1 (sol_task)
+  float* partial;      // their partial states when splits > 1: rows [B H][front][G 64][D + 4]
 };
 
 // Indexed-window protection (plan.hip).

@@ -1,6 +1,7 @@
 """CPU tests of the host contract: validation, plan builder, C-ABI exports."""
 
 import ctypes
+import math
 import os
 import re
 
@@ -144,7 +145,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == _native.ABI_VERSION == 8
+    assert native.sol_abi_version() == _native.ABI_VERSION == 9
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -168,18 +169,18 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     assert rc == -1 and b"scale" in native.sol_last_error()
     attn = lambda index, n, form: native.sol_attention_fwd(  # noqa: E731
         fake, strides, index, n, 1, 193, 317, None, 2, 64, None, None, None, None, fake, fake, fake, fake,
-        None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, form, None)
+        None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, form, None)
     rc = native.sol_attention_fwd(fake, strides, None, 0, 1, 193, 317, None, 2, 64, None, None, None, None,
-                                  fake, fake, None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None,
-                                  None, None, None, None, None, None, 0, None)
+                                  fake, fake, None, None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake,
+                                  None, None, None, None, None, None, None, 0, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
     assert attn(None, 0, 3) == -1 and b"workgroup_form" in native.sol_last_error()
     assert attn(fake, 0, 0) == -1 and b"sequence_length" in native.sol_last_error()
     # Without tiles the keys must qualify for rows mode.
     rows = lambda nk, lengths: native.sol_attention_fwd(  # noqa: E731
         fake, strides, None, 0, 1, 193, nk, lengths, 2, 64, fake, strides, fake, strides, None, fake,
-        fake, fake, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, 0,
-        None)
+        fake, fake, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None,
+        0, None)
     assert rows(63, None) == -1 and b"without tiles" in native.sol_last_error()
     assert rows(317, fake) == -1 and b"without tiles" in native.sol_last_error()
     rc = native.sol_quantize_keys(fake, strides, None, None, 0, 1, 40, 2, 64, 1, fake, fake, None)
@@ -214,6 +215,26 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     assert rc == -1 and b"required" in native.sol_last_error()
     rc = native.sol_plan_protection(fake, None, None, 2, 100, 300, 64, None, 0, fake, None)
     assert rc == -1 and b"required" in native.sol_last_error()
+
+
+def test_split_workspace_only_where_sinks_set_the_launch_end():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("libsol_attn_amd.so not built")
+    size = _native.library().sol_split_workspace_size
+    # 4,096 tokens x 4 heads, D 128, two sink blocks: 4 parts of 16 key
+    # blocks; rows of 128 + 4 floats for sink blocks 0, 1 of 4 (entry, head) pairs.
+    assert size(1, 4096, 4096, 4, 128, 1.0, 128) == 4 * 2 * 64 * 4 * 132 * 4
+    assert size(1, 8192, 8192, 4, 64, 1.0, 192) == 4 * 2 * 64 * 8 * 68 * 4  # 8 parts; block 2 whole
+    # 2 x 4,096 x 16 heads (1,024 query-block pairs): split at beta = +inf only.
+    assert size(2, 4096, 4096, 16, 128, math.inf, 128) == 32 * 2 * 64 * 4 * 132 * 4
+    assert size(2, 4096, 4096, 16, 128, 1.0, 128) == 0
+    assert size(1, 4096, 4096, 4, 128, -math.inf, 128) == 0   # every block exact
+    assert size(1, 4096, 4096, 4, 128, 1.0, 64) == 0          # one sink block
+    assert size(1, 4096, 4096, 4, 128, 1.0, 0) == 0           # no sinks
+    assert size(1, 1024, 1024, 8, 64, 1.0, 128) == 0          # 16 key blocks
+    assert size(1, 84672, 84672, 24, 128, 1.0, 128) == 0      # many rounds of workgroups
+    assert size(1, 4096, 4096, 4, 128, 1.0, 1100) == 0        # sinks over a quarter of the blocks
+    assert size(1, 4096, 600000, 1, 128, 1.0, 128) == 0       # more than one routing segment
 
 
 def test_noalloc_rejects_problems_beyond_its_workspace_without_launching():

@@ -39,7 +39,8 @@ def test_side_stream_matches_default_stream():
 def _capture_cases():
     """(name, setup(monkeypatch) -> call) for the launch shapes: the one-block
     form; the two-block form with the pairing kernels (dynamic-LDS lag kernel
-    included); indexed windows with the fused scatter into out=."""
+    included); query sinks split by key range with the merge kernel; indexed
+    windows with the fused scatter into out=."""
 
     def plain(mp):
         q, k, v = inputs()
@@ -51,6 +52,11 @@ def _capture_cases():
         q, k, v = inputs()
         return lambda: sol_attention(q, k, v, kv_sink_tokens=64)
 
+    def split(mp):
+        q, k, v = inputs()
+        assert _native.library().sol_split_workspace_size(1, 2048, 2048, 4, 128, 1.0, 128) > 0
+        return lambda: sol_attention(q, k, v, kv_sink_tokens=64, query_sink_tokens=128)
+
     def indexed(mp):
         q, k, v = (x[0] for x in inputs())             # NHD [2048, 4, 128]
         rows = torch.stack((torch.arange(0, 700), torch.arange(1000, 1700)))
@@ -59,7 +65,7 @@ def _capture_cases():
         out = torch.zeros_like(q)
         return lambda: sol_attention_indexed(q, k, v, plan, beta=1.0, out=out)
 
-    return {"one-block": plain, "paired": paired, "indexed-scatter": indexed}
+    return {"one-block": plain, "paired": paired, "split-sinks": split, "indexed-scatter": indexed}
 
 
 @pytest.mark.parametrize("case", sorted(_capture_cases()))
