@@ -26,25 +26,44 @@ namespace sol {
 
 namespace {
 
-constexpr int kMeanThreads = 512;  // one 16-byte chunk per thread for up to 32 heads of 128
+constexpr int kMeanThreads = 256;  // four waves
+constexpr int kMeanChunk = 16;     // query blocks per workgroup
 
-// Normalised query-block means: m[((b H + h) D + d) NQB + i] (lag-major rows
-// so that the lag kernel reads one feature of one head contiguously).
+// Normalised query-block means, m[((b H + h) D + d) NQB + i] (lag-major rows
+// so that the lag kernel reads one feature of one head contiguously).  One
+// workgroup per (batch entry, head, 16 consecutive query blocks), in the
+// pooling kernel's load shape: each lane holds 16 rows x 16 bytes of one
+// block in flight (non-temporal: Q is read once here), the four waves take
+// the chunk's blocks in turn, and the lane quarters' partial sums are folded
+// with shuffles.  Each block mean is normalised by its norm over D, staged in
+// LDS, and written out as runs of consecutive blocks per feature.  Heads vary
+// fastest over the grid, so the workgroups in flight read whole token rows.
 template <int D>
 __global__ __launch_bounds__(kMeanThreads) void qblock_means_kernel(PairParams p) {
-  constexpr int DC = D / 8;  // 16-byte chunks per row = threads per head
-  constexpr int kRows = 16;  // row loads in flight per thread
-  const int qb = blockIdx.x, b = blockIdx.y;
-  const int qlen = min(kBlock, p.Tq - qb * kBlock);
-  const int chunks = p.H * DC;
-  for (int c = threadIdx.x; c < chunks; c += blockDim.x) {
-    const int h = c / DC, dc = c % DC;
-    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int r0 = 0; r0 < qlen; r0 += kRows) {
-      u32x4 x[kRows];
-      load_rows16(p.q, b, qb * kBlock + r0, qb * kBlock + qlen - 1, h, 8 * dc, x);
+  constexpr int DC = D / 8;          // 16-byte chunks per row
+  constexpr int LPB = DC * 4;        // lanes per block: 4 quarters of 16 rows
+  constexpr int BPI = kWave / LPB;   // blocks per wave iteration
+  constexpr int NW = kMeanThreads / kWave;
+  constexpr int ITERS = kMeanChunk / (NW * BPI);
+  static_assert(ITERS * NW * BPI == kMeanChunk, "a workgroup covers one chunk");
+  __shared__ float m[kMeanChunk][D + 1];  // padded: the write-out reads columns
+  const int c = blockIdx.x / (p.B * p.H);
+  const int bh = blockIdx.x % (p.B * p.H);
+  const int h = bh % p.H, b = bh / p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int sub = lane / LPB, r4 = (lane % LPB) / DC, dc = lane % DC;
 #pragma unroll
-      for (int r = 0; r < kRows; ++r)
+  for (int it = 0; it < ITERS; ++it) {
+    const int jb = (wave * ITERS + it) * BPI + sub;  // block inside this chunk
+    const int i = c * kMeanChunk + jb;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int qlen = 0;
+    if (i < p.NQB) {
+      qlen = min(kBlock, p.Tq - kBlock * i);
+      u32x4 x[16];
+      load_rows16<16, true>(p.q, b, kBlock * i + 16 * r4, kBlock * i + qlen - 1, h, 8 * dc, x);
+#pragma unroll
+      for (int r = 0; r < 16; ++r)  // rows past the block are zero
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const uint32_t w = x[r][e >> 1];
@@ -54,18 +73,25 @@ __global__ __launch_bounds__(kMeanThreads) void qblock_means_kernel(PairParams p
     float n2 = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      s[e] /= float(qlen);
+      s[e] += __shfl(s[e], lane + DC) + __shfl(s[e], lane + 2 * DC) + __shfl(s[e], lane + 3 * DC);
+      s[e] = qlen > 0 ? s[e] / float(qlen) : 0.f;
       n2 += s[e] * s[e];
     }
-    // The DC threads of one head are consecutive lanes of one wave (chunk
-    // groups start at multiples of DC, and DC divides the wave width).
+    // The DC lanes of quarter 0 of a block are consecutive and DC-aligned.
 #pragma unroll
     for (int off = 1; off < DC; off <<= 1) n2 += __shfl_xor(n2, off);
     const float inv = n2 > 0.f ? rsqrtf(n2) : 0.f;
-    float* dst = p.means + ((int64_t(b) * p.H + h) * D + 8 * dc) * p.NQB + qb;
+    if (r4 == 0)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dst[int64_t(e) * p.NQB] = s[e] * inv;
+      for (int e = 0; e < 8; ++e) m[jb][8 * dc + e] = s[e] * inv;
   }
+  __syncthreads();
+  constexpr int F = kMeanChunk * D / kMeanThreads;  // blocks per thread in the write-out
+  const int d = tid / (kMeanChunk / F), j0 = (tid % (kMeanChunk / F)) * F;
+  float* dst = p.means + (int64_t(bh) * D + d) * p.NQB + c * kMeanChunk;
+#pragma unroll
+  for (int j = j0; j < j0 + F; ++j)
+    if (c * kMeanChunk + j < p.NQB) dst[j] = m[j][d];
 }
 
 // Lag sums of one feature d of one (batch entry, head): thread t holds the
@@ -133,10 +159,11 @@ __global__ __launch_bounds__(kMaxLag) void pair_pick_kernel(PairParams p, int D)
 }  // namespace
 
 hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream) {
+  const unsigned mean_grid = unsigned((p.NQB + kMeanChunk - 1) / kMeanChunk) * unsigned(p.B * p.H);
   if (D == 128)
-    hipLaunchKernelGGL(qblock_means_kernel<128>, dim3(p.NQB, p.B), dim3(kMeanThreads), 0, stream, p);
+    hipLaunchKernelGGL(qblock_means_kernel<128>, dim3(mean_grid), dim3(kMeanThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL(qblock_means_kernel<64>, dim3(p.NQB, p.B), dim3(kMeanThreads), 0, stream, p);
+    hipLaunchKernelGGL(qblock_means_kernel<64>, dim3(mean_grid), dim3(kMeanThreads), 0, stream, p);
   hipLaunchKernelGGL(pair_lag_kernel, dim3(D, p.B * p.H), dim3(kLagThreads), (p.NQB + kLagPad) * sizeof(float),
                      stream, p, D);
   hipLaunchKernelGGL(pair_pick_kernel, dim3(p.B * p.H), dim3(kMaxLag), 0, stream, p, D);
