@@ -145,6 +145,16 @@ void pool_kv_kernel(PoolParams p) {
       float* dst = p.ksum + ((head * nch + c) * 2) * D;
       dst[tid] = s1;
       dst[D + tid] = s2;
+      if (p.NKB <= kPoolChunk) {
+        // One chunk per entry: moments_kernel's fold reduces to these two
+        // divisions, so the moments are written here and its launch is
+        // skipped (launch_pool).
+        const float n = float(nkb);
+        const float m = __fdiv_rn(s1, n);
+        const float v = __fdiv_rn(s2, n) - m * m;
+        p.mean[head * D + tid] = m;
+        p.var[head * D + tid] = v > 0.f ? v : 0.f;
+      }
     }
   } else if (tid < kPoolChunk * DC) {
     const int jb = tid / DC, cc = tid % DC;
@@ -247,7 +257,8 @@ hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
       hipLaunchKernelGGL((pool_kv_kernel<64, 4>), grid, dim3(256), 0, stream, p);
   }
   hipError_t err = hipGetLastError();
-  if (err != hipSuccess || !p.ksum || !p.ctiles) return err;
+  // Single-chunk keys had their moments written by the pooling kernel.
+  if (err != hipSuccess || !p.ksum || !p.ctiles || p.NKB <= kPoolChunk) return err;
   if (D == 128)
     hipLaunchKernelGGL(moments_kernel<128>, dim3(p.B * p.H), dim3(kMomentThreads), 0, stream,
                        p.ksum, p.mean, p.var, p.klen, p.Tk, p.NKB, p.H);
