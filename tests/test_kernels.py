@@ -75,9 +75,12 @@ def centroids(ctiles, nkb):
 
 # Grids of up to 512 chunk workgroups (2 B H ceil(NKB / 64) 4) take the wide
 # pooling form, larger ones the four-wave form: the last two shapes (ragged
-# last block) are the four-wave form's, for D = 64 and 128.
-@pytest.mark.parametrize("shape", [(1, 317, 2, 64), (2, 1089, 3, 128), (1, 1, 1, 64), (2, 4096, 16, 128),
-                                   (1, 10000, 4, 128), (1, 4100, 72, 64), (1, 4033, 68, 128)])
+# last block) are the four-wave form's, for D = 64 and 128.  Keys of at most
+# 16 blocks (one pooling chunk: 317, 1 and exactly 1,024 tokens) get their
+# moments from the pooling kernel itself, longer ones from moments_kernel.
+@pytest.mark.parametrize("shape", [(1, 317, 2, 64), (2, 1089, 3, 128), (1, 1, 1, 64), (1, 1024, 2, 64),
+                                   (2, 4096, 16, 128), (1, 10000, 4, 128), (1, 4100, 72, 64),
+                                   (1, 4033, 68, 128)])
 def test_pooling_and_moments_bit_exact(shape):
     b, t, h, d = shape
     g = torch.Generator().manual_seed(t)
