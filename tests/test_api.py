@@ -325,3 +325,14 @@ def test_frame_window_plan_protection_floor():
         nkb = -(-len(keys[f]) // 64)
         assert int(p.protected_blocks[f, :, :nkb].sum()) == expect
         assert not p.protected_blocks[f, :, nkb:].any()
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits with a message before any GPU work."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 2
+    assert "one GPU only" in res.stderr
