@@ -10,6 +10,7 @@ built this module raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 import os
 
@@ -78,9 +79,15 @@ def _check(status):
         raise RuntimeError(f"SOL HIP call failed ({status}): {msg}")
 
 
+@functools.lru_cache(maxsize=512)
+def _stride_array(batch, token, head):
+    # Read-only once built: every call with the same strides shares one array.
+    return (ctypes.c_int64 * 3)(batch, token, head)
+
+
 def _strides(x, indexed=False):
     s = x.stride()
-    return (ctypes.c_int64 * 3)(0 if indexed else s[0], s[-3], s[-2])
+    return _stride_array(0 if indexed else s[0], s[-3], s[-2])
 
 
 def _ptr(x):
@@ -100,7 +107,12 @@ def _stream(device):
 
 def _aligned(x):
     """Rows start on 16-byte boundaries (base pointer and all strides)."""
-    return x.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in x.stride()[:-1])
+    if x.data_ptr() & 15:
+        return False
+    for s in x.stride()[:-1]:
+        if s & 7:
+            return False
+    return True
 
 
 def _rows(x):
@@ -124,13 +136,15 @@ def rows_mode(k, v, key_index=None, key_lengths=None):
 _ALIGN = 256  # byte alignment of each buffer carved from a workspace
 
 
+@functools.lru_cache(maxsize=256)
 def _carve(sizes):
-    """Byte offsets of consecutive ``_ALIGN``-aligned regions, and their total."""
+    """Byte offsets of consecutive ``_ALIGN``-aligned regions (``sizes``: a tuple of
+    byte counts), and their total."""
     offsets, total = [], 0
     for n in sizes:
         offsets.append(total)
         total += -(-n // _ALIGN) * _ALIGN
-    return offsets, total
+    return tuple(offsets), total
 
 
 def _region(ws, offset, dtype, shape):
@@ -173,7 +187,7 @@ def pool_kv(k, v, key_index=None, moments=True, key_lengths=None, stream=None, v
     sizes += [b * h * -(-nkb // 16) * 2 * d * 4, b * h * d * 4, b * h * d * 4] if moments else [0, 0, 0]
     if qk_int8:
         sizes += [b * h * nkb * BLOCK * d, b * h * nkb * 4]
-    offsets, total = _carve(sizes)
+    offsets, total = _carve(tuple(sizes))
     ws = torch.empty(total, device=dev, dtype=torch.uint8)
     base = ws.data_ptr()
     ctiles, tiles = base + offsets[0], None if rows else base + offsets[1]
@@ -265,11 +279,16 @@ def pair_strides(q, rows=None, min_blocks=None, stream=None):
 SPLIT_SINKS = True
 
 
+@functools.lru_cache(maxsize=256)
+def _split_size(b, nq, nk, h, d, beta, q_sink):
+    return library().sol_split_workspace_size(b, nq, nk, h, d, beta, q_sink)
+
+
 def split_workspace(b, nq, nk, h, d, beta, q_sink, device):
     """The split workspace of an attention launch (None when it is not split)."""
     if not SPLIT_SINKS:
         return None
-    size = library().sol_split_workspace_size(b, nq, nk, h, d, float(beta), int(q_sink))
+    size = _split_size(b, nq, nk, h, d, float(beta), int(q_sink))
     return torch.empty(size // 4, device=device, dtype=torch.float32) if size else None
 
 
