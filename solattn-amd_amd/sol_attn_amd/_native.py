@@ -247,31 +247,56 @@ PAIRING = True
 PAIR_MIN_QUERY_BLOCKS = 8192
 
 
+def _pair_buffers(q, rows, min_blocks):
+    """``(q, workspace, strides)`` for a pairing launch, allocated on the current
+    stream, or None when pairing does not apply (see :func:`pair_strides`)."""
+    b, nq = rows.shape if rows is not None else q.shape[:2]
+    h, d = q.shape[-2:]
+    if b * h * -(-nq // BLOCK) < min_blocks:
+        return None
+    size = library().sol_pair_workspace_size(b, nq, h, d)
+    if size == 0:
+        return None
+    return (_rows(q), torch.empty(size // 4, device=q.device, dtype=torch.float32),
+            torch.empty((b, h), device=q.device, dtype=torch.int32))
+
+
+def _pair_launch(q, rows, work, strides, stream):
+    indexed = rows is not None
+    b, nq = rows.shape if indexed else q.shape[:2]
+    h, d = q.shape[-2:]
+    _check(library().sol_pair_strides(q.data_ptr(), _strides(q, indexed), _ptr(rows),
+                                      q.shape[0] if indexed else 0, b, nq, h, d,
+                                      work.data_ptr(), strides.data_ptr(), stream))
+
+
 def pair_strides(q, rows=None, min_blocks=None, stream=None):
     """Per-(entry, head) query-block pairing strides (int32 ``[B, H]``), or None
     when pairing does not apply: fewer than ``min_blocks`` query blocks in
     all (by default PAIR_MIN_QUERY_BLOCKS), or a sequence outside the
     library's 4 .. 8192 query blocks."""
-    indexed = rows is not None
-    b, nq = rows.shape if indexed else q.shape[:2]
-    h, d = q.shape[-2:]
-    if min_blocks is None:
-        min_blocks = PAIR_MIN_QUERY_BLOCKS
-    if b * h * -(-nq // BLOCK) < min_blocks:
+    bufs = _pair_buffers(q, rows, PAIR_MIN_QUERY_BLOCKS if min_blocks is None else min_blocks)
+    if bufs is None:
         return None
-    lib = library()
-    size = lib.sol_pair_workspace_size(b, nq, h, d)
-    if size == 0:
-        return None
-    q = _rows(q)
-    if stream is None:
-        stream = _stream(q.device)
-    work = torch.empty(size // 4, device=q.device, dtype=torch.float32)
-    strides = torch.empty((b, h), device=q.device, dtype=torch.int32)
-    _check(lib.sol_pair_strides(q.data_ptr(), _strides(q, indexed), _ptr(rows),
-                                q.shape[0] if indexed else 0, b, nq, h, d,
-                                work.data_ptr(), strides.data_ptr(), stream))
+    qr, work, strides = bufs
+    _pair_launch(qr, rows, work, strides, _stream(q.device) if stream is None else stream)
     return strides
+
+
+# Run the pairing kernels (they read Q only) on a second stream of the same
+# device, concurrently with pooling (K and V only), joined back to the
+# caller's stream before the attention launch.  False runs them on the
+# caller's stream.  Results are identical either way.
+OVERLAP_PAIRING = True
+_side_streams = {}
+
+
+def _side_stream(device):
+    """One extra stream per device, at the default priority."""
+    side = _side_streams.get(device.index)
+    if side is None:
+        side = _side_streams[device.index] = torch.cuda.Stream(device=device)
+    return side
 
 
 # Split the query-sink tiles of short launches over several workgroups
@@ -292,14 +317,19 @@ def split_workspace(b, nq, nk, h, d, beta, q_sink, device):
     return torch.empty(size // 4, device=device, dtype=torch.float32) if size else None
 
 
+_UNSET = object()
+
+
 def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows=None,
-           debug=False, out=None, stats=True, stream=None):
+           debug=False, out=None, stats=True, stream=None, strides=_UNSET):
     """Routing + attention over pooled keys (the ``_sol`` launch of ``kernels.py:218-224``).
 
     ``pooled`` is the dict returned by :func:`pool_kv`.  ``rows`` (indexed
     windows) gathers the query rows.  With ``out`` (a contiguous BF16
     ``[N, H, D]`` tensor, indexed windows only) query i of window w is stored
     at ``out[rows[w, i]]`` instead of into a new ``[W, nq, H, D]`` tensor.
+    ``strides``: pairing strides already computed (:func:`pair_strides`; None
+    pairs adjacent blocks); by default they are computed here.
     Returns ``(out, counts, dbg)``; ``counts`` is None unless ``stats`` and
     ``dbg`` is None unless ``debug``.
     """
@@ -331,7 +361,8 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     prot = None
     if protection is not None:
         prot = protection.contiguous().view(torch.uint8)
-    strides = pair_strides(q, rows, stream=stream) if PAIRING else None
+    if strides is _UNSET:
+        strides = pair_strides(q, rows, stream=stream) if PAIRING else None
     split = split_workspace(b, nq, nk, h, d, beta, q_sink, dev)
     kr, vr = pooled["k"], pooled["v"]
     _check(lib.sol_attention_fwd(
@@ -378,12 +409,27 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
             counts = torch.full((b, -(-nq // BLOCK), h), -(-k.shape[1] // BLOCK), device=q.device, dtype=torch.int32)
         return dense, counts
     stream = _stream(q.device)
+    strides, pairing = _UNSET, None
+    if PAIRING and OVERLAP_PAIRING:
+        # Buffers come from the caller's stream and stay referenced until the
+        # join below, so no other allocation can reuse them while the side
+        # stream still works on them.
+        pairing = _pair_buffers(q, rows, PAIR_MIN_QUERY_BLOCKS)
+        strides = None
+        if pairing is not None:
+            main, side = torch.cuda.current_stream(q.device), _side_stream(q.device)
+            side.wait_stream(main)
+            _pair_launch(pairing[0], rows, pairing[1], pairing[2], side.cuda_stream)
+            strides = pairing[2]
     pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths,
                      stream=stream, views=debug, qk_int8=qk_precision == "int8")
     if threshold_estimator == "full_covariance" and not math.isinf(beta):
         key_covariance(pooled, stream)
+    if pairing is not None:
+        main.wait_stream(side)
     out, counts, dbg = attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection, rows,
-                              debug, out, stats, stream)
+                              debug, out, stats, stream, strides=strides)
+    del pairing
     if debug:
         dbg.update(pooled)
         return out, counts, dbg

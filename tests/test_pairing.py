@@ -95,6 +95,40 @@ def test_pairing_never_changes_results(beta, d, monkeypatch):
         assert torch.equal(counts, ref_stats.exact_blocks), s
 
 
+def test_pairing_on_the_side_stream_matches_the_caller_stream(monkeypatch):
+    """The pairing kernels run on a second stream of the device, concurrently
+    with pooling, and join the caller's stream before attention
+    (OVERLAP_PAIRING).  Run on the caller's stream instead, or called from a
+    non-default caller stream, the results are bit-identical."""
+    monkeypatch.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", 2)
+    q, k, v = (frames(8, 9, seed=s).cuda() for s in (3, 4, 5))
+    x = [frames(10, 6, seed=s)[0].cuda() for s in (6, 7, 8)]
+    t = x[0].shape[0]
+    rows = torch.stack((torch.arange(0, t // 2), torch.arange(t // 2, t)))
+    keys = [torch.arange(0, t - 64), torch.arange(64, t - 128)]
+    plan = IndexedPlan.create(rows, keys, t, protected_ranges=((0, 64),), local_tokens=64).to("cuda")
+    assert _native.pair_strides(q) is not None and _native.pair_strides(x[0], plan.rows) is not None
+
+    def run():
+        out, stats = sol_attention(q, k, v, beta=1.0, kv_sink_tokens=64, return_stats=True)
+        win, win_stats = sol_attention_indexed(*x, plan, beta=1.0, return_stats=True)
+        return out, stats.exact_blocks, win, win_stats.exact_blocks
+
+    ref = run()
+    monkeypatch.setattr(_native, "OVERLAP_PAIRING", False)
+    serial = run()
+    monkeypatch.setattr(_native, "OVERLAP_PAIRING", True)
+    caller = torch.cuda.Stream()
+    caller.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(caller):
+        on_caller = run()
+    torch.cuda.current_stream().wait_stream(caller)
+    torch.cuda.synchronize()
+    for a, b, c in zip(ref, serial, on_caller):
+        assert torch.equal(a, b) and torch.equal(a, c)
+
+
 def test_indexed_windows_pair_per_window(monkeypatch):
     monkeypatch.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 4)
     monkeypatch.setattr(_native, "WORKGROUP_FORM", 2)  # two-block workgroups (this launch is small)

@@ -2,10 +2,12 @@
 the current stream of the device).
 
 On a side stream the call gives the default stream's results.  Under HIP
-graph capture every launch must be on the capturing stream (a launch on
-another stream makes the capture fail), and the captured graph replays to
-the eager result, checked on every replay with eager work and
-synchronisation in between.
+graph capture every launch must be on the capturing stream or on a stream
+that joined the capture through an event (the pairing kernels' own stream
+forks from the caller's stream and joins it again; a launch on any other
+stream makes the capture fail), and the captured graph replays to the eager
+result, checked on every replay with eager work and synchronisation in
+between.
 """
 
 import pytest
