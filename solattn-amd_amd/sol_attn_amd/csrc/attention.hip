@@ -56,7 +56,15 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
   u32x4 k0[KT], k1[KT];
 #pragma unroll
   for (int ks = 0; ks < KT; ++ks) k0[ks] = fl.k(buf, 0, ks);
-  HalfSoftmax<D> h0, h1;
+  // The raw scores of half t again (FastHalf::resolve), from the tile still in LDS.
+  auto raw = [&](int t) {
+    const FragLane<D> fr(fresh(col), fresh(hh));
+    f32x16 s = BIASED ? bias(t) : zero16();
+#pragma unroll
+    for (int ks = 0; ks < KT; ++ks) s = mfma32x32x16(as_bf16x8(fr.k(buf, t, ks)), qf[ks], s);
+    return s;
+  };
+  FastHalf<D> h0, h1;
   h0.s = BIASED ? bias(0) : zero16();
   chunk_end();
 #pragma unroll
@@ -80,7 +88,7 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
     refill.template after_step<2 * KT>(KT + ks);
     chunk_end();
   }
-  if (h0.rescale) rescale_acc<D>(st, h0.alpha);
+  h0.resolve(st, c, [&] { return raw(0); });
   u32x4 vb[2][DT];
 #pragma unroll
   for (int f = 0; f < 2 * DT; ++f) {
@@ -90,7 +98,7 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
     h1.template part<2 * DT>(f, st, c);
     chunk_end();
   }
-  if (h1.rescale) rescale_acc<D>(st, h1.alpha);
+  h1.resolve(st, c, [&] { return raw(1); });
 #pragma unroll
   for (int f = 0; f < 2 * DT; ++f) {
     const int c4 = f / DT, dt = f % DT;

@@ -454,6 +454,74 @@ struct HalfSoftmax {
   }
 };
 
+// Common case of HalfSoftmax without its max pass: the probabilities
+// p = exp2(s c - m) are formed against the running max m as it stands, and
+// the row sum tells whether that was what HalfSoftmax would have done.  If
+// no lane's sum exceeds 255 (or, before any key, 0), every p is below 2^8,
+// i.e. every s c - m < log2(255) < kRescaleSlack, so HalfSoftmax would not
+// have moved m and would have formed these same p, den += lsum, with acc
+// untouched: the results are bit-identical.  Otherwise `redo` is set (a
+// wave-uniform ballot) and the caller re-forms the half's raw scores and
+// runs HalfSoftmax on them (resolve).  The stages are:
+// 4 x 4 probabilities and the row sum; the redo ballot; BF16 packing; den.
+constexpr float kFastSumMax = 255.f;
+
+template <int D>
+struct FastHalf {
+  f32x16 s;
+  float lsum, neg_m, thr;
+  bool redo;
+  bf16x8 pw[2];
+
+  __device__ __forceinline__ void stage(int k, State<D>& st, float c) {
+    if (k < 4) {
+      if (k == 0) {
+        const bool none = st.m == kNegInf;  // nothing yet: p = exp2(s c), and any key moves m
+        neg_m = none ? 0.f : -st.m;
+        thr = none ? 0.f : kFastSumMax;
+        lsum = 0.f;
+      }
+#pragma unroll
+      for (int e = 4 * k; e < 4 * (k + 1); ++e) {
+        const float pe = fast_exp2(fmaf(s[e], c, neg_m));
+        s[e] = pe;
+        lsum += pe;
+      }
+    } else if (k == 4) {
+      redo = __builtin_amdgcn_ballot_w64(lsum > thr) != 0;
+    } else if (k == 5) {
+      pw[0] = pack8(s, 0);
+      pw[1] = pack8(s, 8);
+      pin(pw[0]);
+      pin(pw[1]);
+    } else if (k == 7) {
+      st.den = redo ? st.den : st.den + lsum;
+      pin(st.den);
+    }
+  }
+  template <int N>
+  __device__ __forceinline__ void part(int k, State<D>& st, float c) {
+#pragma unroll
+    for (int i = k * 8 / N; i < (k + 1) * 8 / N; ++i) stage(i, st, c);
+  }
+  __device__ __forceinline__ bf16x8 pb(int c4) const { return pw[c4]; }
+  // The uncommon case: raw() re-forms the half's scores, HalfSoftmax runs
+  // on them (max, rescale decision, probabilities, den), and acc is rescaled
+  // if it moved m.
+  template <typename Raw>
+  __device__ __forceinline__ void resolve(State<D>& st, float c, Raw raw) {
+    if (redo) {
+      HalfSoftmax<D> full;
+      full.s = raw();
+#pragma unroll
+      for (int i = 0; i < 8; ++i) full.stage(i, st, c);
+      if (full.rescale) rescale_acc<D>(st, full.alpha);
+      pw[0] = full.pw[0];
+      pw[1] = full.pw[1];
+    }
+  }
+};
+
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 // This lane's offsets of its MFMA operand reads inside a K + V tile pair
