@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 9
+#define SOL_ABI_VERSION 10
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_TOKENS (1ll << 25) /* key_tokens of one pooling call (2^19 key blocks) */
 
@@ -108,13 +108,17 @@ int64_t sol_pair_workspace_size(int64_t batch, int64_t query_tokens, int64_t hea
  * alike normalised query-block means (routing follows those means).  s = 1
  * is the adjacent pairing.  Q and query_index as in sol_attention_fwd;
  * workspace: sol_pair_workspace_size() bytes, 16-byte aligned; strides:
- * int32 [batch, heads].  The pairing never changes results, only the
- * schedule.  No counterpart in the reference (one Triton program per query
- * block, no pairing). */
+ * int32 [batch, heads].  query_means: NULL, or fp32 [batch, heads,
+ * ceil(query_tokens / 64), head_dim] receiving the FP32 query-block means
+ * (torch's cascade summation order: bit-identical to the reference oracle's
+ * `_means`, reference.py:13-15), which sol_attention_fwd's routing kernel
+ * can take instead of reading Q again.  The pairing never changes results,
+ * only the schedule.  No counterpart in the reference (one Triton program
+ * per query block, no pairing). */
 int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* query_index,
                      int64_t sequence_length, int64_t batch, int64_t query_tokens,
                      int64_t heads, int64_t head_dim, void* workspace, int32_t* strides,
-                     void* stream);
+                     float* query_means, void* stream);
 
 /* Workspace bytes of sol_key_covariance (0: unsupported shape). */
 int64_t sol_key_covariance_workspace_size(int64_t batch, int64_t heads, int64_t head_dim);
@@ -146,7 +150,20 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
 int64_t sol_split_workspace_size(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
                                  int64_t head_dim, double beta, int64_t query_sink_tokens);
 
-/* Fused routing + attention over the pooled keys of sol_pool_kv.
+/* Bytes of the route_workspace sol_attention_fwd may take (0 for beta =
+ * -INFINITY, which selects every block, or an invalid shape): the routing
+ * decisions, uint32 [batch, heads, ceil(query_tokens / 64), ceil(NKB / 32)]
+ * (bit j of word w: key block 32 w + j), written by the routing kernel and
+ * read by the attention kernel of the same call. */
+int64_t sol_route_workspace_size(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                                 double beta);
+
+/* Routing + attention over the pooled keys of sol_pool_kv.  With a
+ * route_workspace, a routing kernel forms the cutoffs and every (query block,
+ * key block) decision first and the attention kernel reads them; without
+ * one, the attention kernel routes each centroid tile as it streams it.
+ * Decisions agree to the routing band (FP32 summation order), outputs are
+ * otherwise the same.
  * Replaces the `_threshold` and `_sol` launches of `launch_sol`
  * (kernels.py:203-225; kernels kernels.py:52-64 and 101-182).
  * beta: finite, -INFINITY (every block exact) or +INFINITY (protected blocks
@@ -162,6 +179,13 @@ int64_t sol_split_workspace_size(int64_t batch, int64_t query_tokens, int64_t ke
  * sol_split_workspace_size(batch, query_tokens, key_tokens, heads, head_dim,
  * beta, query_sink_tokens) bytes when that is nonzero; split and unsplit
  * calls agree to rounding (the parts' states merge in a fixed order).
+ * route_workspace: NULL (routing inside the attention kernel, the better
+ * choice for short launches) or 16-byte aligned device memory of
+ * sol_route_workspace_size(batch, query_tokens, key_tokens, heads, beta)
+ * bytes (routing kernel first: it saves the attention kernel a routing pass
+ * and a barrier per centroid tile on long key sequences).  query_means: NULL
+ * (the routing kernel forms the query-block means from Q) or the query_means
+ * output of sol_pair_strides for the same Q (only with route_workspace).
  * out: contiguous BF16 [batch, query_tokens, heads, head_dim]; or, when
  * out_index (int64 [batch, query_tokens], device) is given, a contiguous BF16
  * [N, heads, head_dim] whose row out_index[b * query_tokens + t] receives
@@ -196,7 +220,8 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       const void* tiles, const void* ctiles,
                       const float* key_mean, const float* key_var, const float* key_cov,
                       const uint8_t* protection, const int32_t* pair_strides, void* split_workspace,
-                      double scale, double beta, int64_t local_blocks,
+                      void* route_workspace, const float* query_means, double scale, double beta,
+                      int64_t local_blocks,
                       int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
@@ -265,7 +290,7 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides,
  * and V (rows mode), except for fewer than 64 keys or token strides of 2^24
  * elements or more, where the block tiles (4 * head_dim bytes per key token
  * and head) join them, and the split workspace when the problem is split
- * (sol_split_workspace_size).  Problems needing more than SOL_NOALLOC_SCRATCH_BYTES
+ * (sol_split_workspace_size); routing runs inside the attention kernel.  Problems needing more than SOL_NOALLOC_SCRATCH_BYTES
  * (128 MiB) return SOL_ERR_UNSUPPORTED before any GPU work.  Every call on
  * one GPU shares that GPU's array: calls that overlap on one GPU (different
  * streams or threads) race and must be serialised by the caller. */

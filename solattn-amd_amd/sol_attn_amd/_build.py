@@ -17,7 +17,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.abspath(os.path.join(PKG, "..", "..", "include"))
 LIB_NAME = "libsol_attn_amd.so"
-SOURCES = ("pool.hip", "attention.hip", "pairing.hip", "plan.hip", "covariance.hip", "quant.hip", "capi.hip")
+SOURCES = ("pool.hip", "route.hip", "attention.hip", "pairing.hip", "plan.hip", "covariance.hip", "quant.hip", "capi.hip")
 # pool.hip reproduces torch's rounding step for step: no multiply-add fusion.
 EXTRA_FLAGS = {"pool.hip": ["-ffp-contract=off"]}
 ARCH = "gfx950"

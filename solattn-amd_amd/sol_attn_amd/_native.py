@@ -17,7 +17,7 @@ import os
 import torch
 
 BLOCK = 64
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -36,11 +36,12 @@ _SIGNATURES = {
     "sol_pool_kv": ([_p, _i64p, _p, _i64p, _p, _p, _i64, _i64, _i64, _i64, _i64,
                      _p, _p, _p, _p, _p, _p], ctypes.c_int),
     "sol_pair_workspace_size": ([_i64, _i64, _i64, _i64], ctypes.c_int64),
-    "sol_pair_strides": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "sol_pair_strides": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p, _p], ctypes.c_int),
     "sol_split_workspace_size": ([_i64, _i64, _i64, _i64, _i64, _dbl, _i64], ctypes.c_int64),
+    "sol_route_workspace_size": ([_i64, _i64, _i64, _i64, _dbl], ctypes.c_int64),
     "sol_attention_fwd": ([_p, _i64p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64,
                            _p, _i64p, _p, _i64p,
-                           _p, _p, _p, _p, _p, _p, _p, _p,
+                           _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
                            _p, _p, _p, _p, _p, _p, _p, _p, _int, _p], ctypes.c_int),
     "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
@@ -248,8 +249,10 @@ PAIR_MIN_QUERY_BLOCKS = 8192
 
 
 def _pair_buffers(q, rows, min_blocks):
-    """``(q, workspace, strides)`` for a pairing launch, allocated on the current
-    stream, or None when pairing does not apply (see :func:`pair_strides`)."""
+    """``(q, workspace, strides, query_means)`` for a pairing launch, allocated
+    on the current stream, or None when pairing does not apply (see
+    :func:`pair_strides`).  ``query_means``: fp32 ``[B, H, NQB, D]``, the FP32
+    query-block means the pairing pass also writes (the routing kernel's Qc)."""
     b, nq = rows.shape if rows is not None else q.shape[:2]
     h, d = q.shape[-2:]
     if b * h * -(-nq // BLOCK) < min_blocks:
@@ -258,16 +261,28 @@ def _pair_buffers(q, rows, min_blocks):
     if size == 0:
         return None
     return (_rows(q), torch.empty(size // 4, device=q.device, dtype=torch.float32),
-            torch.empty((b, h), device=q.device, dtype=torch.int32))
+            torch.empty((b, h), device=q.device, dtype=torch.int32),
+            torch.empty((b, h, -(-nq // BLOCK), d), device=q.device, dtype=torch.float32))
 
 
-def _pair_launch(q, rows, work, strides, stream):
+def _pair_launch(q, rows, work, strides, means, stream):
     indexed = rows is not None
     b, nq = rows.shape if indexed else q.shape[:2]
     h, d = q.shape[-2:]
     _check(library().sol_pair_strides(q.data_ptr(), _strides(q, indexed), _ptr(rows),
                                       q.shape[0] if indexed else 0, b, nq, h, d,
-                                      work.data_ptr(), strides.data_ptr(), stream))
+                                      work.data_ptr(), strides.data_ptr(), _ptr(means), stream))
+
+
+def _pairing(q, rows=None, stream=None):
+    """``(strides, query_means)`` of a pairing launch on ``stream``, or
+    ``(None, None)`` when pairing does not apply (:func:`pair_strides`)."""
+    bufs = _pair_buffers(q, rows, PAIR_MIN_QUERY_BLOCKS)
+    if bufs is None:
+        return None, None
+    qr, work, strides, means = bufs
+    _pair_launch(qr, rows, work, strides, means, _stream(q.device) if stream is None else stream)
+    return strides, means
 
 
 def pair_strides(q, rows=None, min_blocks=None, stream=None):
@@ -278,8 +293,8 @@ def pair_strides(q, rows=None, min_blocks=None, stream=None):
     bufs = _pair_buffers(q, rows, PAIR_MIN_QUERY_BLOCKS if min_blocks is None else min_blocks)
     if bufs is None:
         return None
-    qr, work, strides = bufs
-    _pair_launch(qr, rows, work, strides, _stream(q.device) if stream is None else stream)
+    qr, work, strides, _ = bufs
+    _pair_launch(qr, rows, work, strides, None, _stream(q.device) if stream is None else stream)
     return strides
 
 
@@ -309,6 +324,31 @@ def _split_size(b, nq, nk, h, d, beta, q_sink):
     return library().sol_split_workspace_size(b, nq, nk, h, d, beta, q_sink)
 
 
+@functools.lru_cache(maxsize=256)
+def _route_size(b, nq, nk, h, beta):
+    return library().sol_route_workspace_size(b, nq, nk, h, beta)
+
+
+# Route in a pre-pass kernel (sol_attention_fwd's route_workspace) when the
+# pairing pass supplied the FP32 query-block means and the keys span at least
+# ROUTE_MIN_CENTROID_TILES centroid tiles of 64 blocks; otherwise the
+# attention kernel routes tile by tile as it streams the centroid tiles.
+# The routing kernel saves that per-tile work and its barrier on long key
+# sequences; short launches are latency-bound, and a second launch would
+# cost more than it saves.  False never uses the routing kernel; "always"
+# uses it for every launch at finite or +inf beta (forming the query means
+# from Q when no pairing pass supplied them).  Decisions agree to the routing
+# band either way.
+ROUTE_PREPASS = True
+ROUTE_MIN_CENTROID_TILES = 4
+
+
+def route_workspace(b, nq, nk, h, beta, device):
+    """The routing masks of an attention launch (None at beta = -inf)."""
+    size = _route_size(b, nq, nk, h, float(beta))
+    return torch.empty(size // 4, device=device, dtype=torch.int32) if size else None
+
+
 def split_workspace(b, nq, nk, h, d, beta, q_sink, device):
     """The split workspace of an attention launch (None when it is not split)."""
     if not SPLIT_SINKS:
@@ -321,7 +361,7 @@ _UNSET = object()
 
 
 def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows=None,
-           debug=False, out=None, stats=True, stream=None, strides=_UNSET):
+           debug=False, out=None, stats=True, stream=None, strides=_UNSET, query_means=None):
     """Routing + attention over pooled keys (the ``_sol`` launch of ``kernels.py:218-224``).
 
     ``pooled`` is the dict returned by :func:`pool_kv`.  ``rows`` (indexed
@@ -329,7 +369,10 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     ``[N, H, D]`` tensor, indexed windows only) query i of window w is stored
     at ``out[rows[w, i]]`` instead of into a new ``[W, nq, H, D]`` tensor.
     ``strides``: pairing strides already computed (:func:`pair_strides`; None
-    pairs adjacent blocks); by default they are computed here.
+    pairs adjacent blocks); by default they are computed here, with the
+    query-block means.  ``query_means``: the FP32 query-block means of the
+    pairing pass (``_pairing``), which let routing run as a pre-pass
+    (ROUTE_PREPASS).
     Returns ``(out, counts, dbg)``; ``counts`` is None unless ``stats`` and
     ``dbg`` is None unless ``debug``.
     """
@@ -362,15 +405,22 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     if protection is not None:
         prot = protection.contiguous().view(torch.uint8)
     if strides is _UNSET:
-        strides = pair_strides(q, rows, stream=stream) if PAIRING else None
+        strides, query_means = _pairing(q, rows, stream) if PAIRING else (None, None)
     split = split_workspace(b, nq, nk, h, d, beta, q_sink, dev)
+    route = None
+    if beta != -math.inf and (ROUTE_PREPASS == "always" or (
+            ROUTE_PREPASS and query_means is not None and -(-nkb // BLOCK) >= ROUTE_MIN_CENTROID_TILES)):
+        route = route_workspace(b, nq, nk, h, beta, dev)
+    else:
+        query_means = None
     kr, vr = pooled["k"], pooled["v"]
     _check(lib.sol_attention_fwd(
         q.data_ptr(), _strides(q, indexed), _ptr(rows), q.shape[0] if indexed else 0,
         b, nq, nk, _ptr(pooled["key_lengths"]), h, d,
         _ptr(kr), None if kr is None else _strides(kr), _ptr(vr), None if vr is None else _strides(vr),
         pooled["tiles_ptr"], pooled["ctiles_ptr"], pooled["mean_ptr"], pooled["var_ptr"], pooled["cov_ptr"],
-        _ptr(prot), _ptr(strides), _ptr(split), float(scale), float(beta), int(local), int(kv_sink), int(q_sink),
+        _ptr(prot), _ptr(strides), _ptr(split), _ptr(route), _ptr(query_means), float(scale), float(beta),
+        int(local), int(kv_sink), int(q_sink),
         out.data_ptr(), _ptr(rows if scatter else None), _ptr(counts),
         _ptr(dbg and dbg["selected"]), _ptr(dbg and dbg["proxy"]), _ptr(dbg and dbg["cutoff"]),
         pooled["k8_ptr"], pooled["k8_scale_ptr"], WORKGROUP_FORM, stream))
@@ -409,7 +459,7 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
             counts = torch.full((b, -(-nq // BLOCK), h), -(-k.shape[1] // BLOCK), device=q.device, dtype=torch.int32)
         return dense, counts
     stream = _stream(q.device)
-    strides, pairing = _UNSET, None
+    strides, pairing, means = _UNSET, None, None
     if PAIRING and OVERLAP_PAIRING:
         # Buffers come from the caller's stream and stay referenced until the
         # join below, so no other allocation can reuse them while the side
@@ -419,8 +469,8 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
         if pairing is not None:
             main, side = torch.cuda.current_stream(q.device), _side_stream(q.device)
             side.wait_stream(main)
-            _pair_launch(pairing[0], rows, pairing[1], pairing[2], side.cuda_stream)
-            strides = pairing[2]
+            _pair_launch(pairing[0], rows, pairing[1], pairing[2], pairing[3], side.cuda_stream)
+            strides, means = pairing[2], pairing[3]
     pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths,
                      stream=stream, views=debug, qk_int8=qk_precision == "int8")
     if threshold_estimator == "full_covariance" and not math.isinf(beta):
@@ -428,7 +478,7 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
     if pairing is not None:
         main.wait_stream(side)
     out, counts, dbg = attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection, rows,
-                              debug, out, stats, stream, strides=strides)
+                              debug, out, stats, stream, strides=strides, query_means=means)
     del pairing
     if debug:
         dbg.update(pooled)

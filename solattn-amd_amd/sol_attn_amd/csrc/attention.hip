@@ -470,7 +470,7 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   constexpr int kMaskWords = kMaxKeyBlocks / 32;
   static_assert(R * S::TILE >= G * kBlock * S::KS, "Q staging must fit in the ring");
   __shared__ __align__(256) uint16_t ring[R * S::TILE];  // Q staging, then the tile ring
-  __shared__ float s_qm[G][D];
+  __shared__ float s_qm[G][D];  // in-kernel routing: query means, partial sums, cutoffs
   __shared__ float s_red[G][4];
   __shared__ float s_cut[G];
   __shared__ uint32_t s_mask[G][kMaskWords];
@@ -557,8 +557,10 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
     csq = p.scale_log2 * __fdiv_rn(amax, 127.f);
   }
 
-  // 2. Query mean and cutoff per query block (sums in torch's cascade order).
-  if (p.force == 0) {
+  // 2. In-kernel routing (no routing masks given): query mean and cutoff per
+  // query block (sums in torch's cascade order).
+  const bool routed = p.mask != nullptr;  // decisions precomputed by route_kernel
+  if (p.force == 0 && !routed) {
     const int qlen = live ? min(kBlock, p.Tq - qb * kBlock) : 1;
     if (lt < D) {
       float tot = 0.f;
@@ -604,7 +606,9 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   }
   __syncthreads();  // cutoffs published; Q staging is dead and the ring is free
   const int64_t dbg_row = ((int64_t(b) * p.NQB + qb) * p.H + h) * p.NKB;
-  if (live && p.dbg_cutoff && lt == 0 && task.split == 0)
+  // With precomputed routing, route_kernel wrote the cutoffs and decisions
+  // and their diagnostics (every block exact at beta = -inf needs none).
+  if (live && p.dbg_cutoff && lt == 0 && task.split == 0 && (!routed || p.force == 1))
     p.dbg_cutoff[(int64_t(b) * p.NQB + qb) * p.H + h] =
         p.force == 0 ? s_cut[qg] * p.scale : (p.force == 1 ? kNegInf : -kNegInf);
 
@@ -637,55 +641,78 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
       }
       __syncthreads();
     } else {
-      // 3. Centroid pass.  Per tile: routing of the tile's 64 blocks for every
-      // query block of the group -- wave w scores blocks 32 (w & 1) + (lane & 31)
-      // of query block w >> 1 over feature half lane >> 5, the halves summed
-      // across the lane pair -- into the LDS bitmask (bit j - seg); a barrier
-      // publishes the mask; then the approximated blocks' contributions.
+      // 3. Centroid pass over the segment's centroid tiles (the tiles holding
+      // blocks [r0, r1)).  Routing decisions come from route_kernel's masks
+      // (loaded into the LDS bitmask, bit j - seg, before the stream) or are
+      // formed here, tile by tile.
       const uint16_t* ctiles = p.ctiles + head * p.NCT * S::TILE;
-      auto process = [&](const uint16_t* buf, int ct, const auto& refill) {
-        const int r = fresh(32 * qh + col);  // centroid row inside the tile
-        const int j = kBlock * ct + r;
-        bool sel = false;
-        if (live && j >= seg + r0 && j < seg + r1) {
-          if (p.force == 0) {
-            const int c0 = fresh(hh) * (S::DC / 2);  // first 16-byte chunk of this lane's feature half
-            float part[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int c = 0; c < S::DC / 2; ++c) {
-              const int cc = c0 + c;
-              const u32x4 x = *reinterpret_cast<const u32x4*>(buf + TL::k_offset(r, cc));
-#pragma unroll
-              for (int e = 0; e < 8; ++e) {
-                const uint32_t w = x[e >> 1];
-                part[e & 3] = fmaf(s_qm[qg][8 * cc + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)),
-                                   part[e & 3]);
-              }
-            }
-            const float proxy = pair_sum((part[0] + part[1]) + (part[2] + part[3]));
-            sel = proxy > s_cut[qg];
-            if (p.dbg_proxy && hh == 0) p.dbg_proxy[dbg_row + j] = proxy * p.scale;
-          }
-          sel = sel || (p.local_blocks >= 0 && abs(j - qb) <= p.local_blocks) || j < p.kv_sink_blocks ||
-                qb < p.q_sink_blocks;
-          if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * p.NKB + j] != 0;
-          if (p.dbg_selected && hh == 0) p.dbg_selected[dbg_row + j] = sel ? 1 : 0;
-        }
-        const uint64_t bal = __ballot(sel);
-        if (lane == 0) s_mask[qg][2 * (ct - ct0) + qh] = uint32_t(bal);
-        lds_barrier();  // publishes the mask words
-        // Branch-free: a tile with no approximated block for this query block
-        // (or a query block past the end) has every score at -inf and adds
-        // nothing.
-        const uint64_t approx = live ? tile_approx(s_mask[qg], ct - ct0, r0, r1) : 0ull;
-        centroid_tile<D>(st, buf, ct, approx, tk, qf, col, hh, scale_log2, refill);
-      };
       auto always = [](int) { return true; };
-      const int ct_lo = ct0 + r0 / kBlock;  // the centroid tiles holding blocks [r0, r1)
+      const int ct_lo = ct0 + r0 / kBlock;
       const int nct = r1 > r0 ? ct0 + (r1 - 1) / kBlock - ct_lo + 1 : 0;
-      tile_stream<D, NT, R>(ring, nct, RangeCursor{ct_lo},
-                            bf16_refills<D, NT>([=](int ct) { return ctiles + int64_t(ct) * S::TILE; }, wave, lane),
-                            tile_runs(always, process, process), process, wave, lane);
+      const auto crefill = bf16_refills<D, NT>([=](int ct) { return ctiles + int64_t(ct) * S::TILE; }, wave, lane);
+      if (routed) {
+        const int nwords = (snkb + 31) / 32;
+        for (int i = tid; i < G * nwords; i += NT) {
+          const int g = i / nwords, w = i % nwords;
+          const int qbg = slot_block(qb0 + g, p.NQB, stride);
+          s_mask[g][w] = qbg < p.NQB ? p.mask[((head * p.NQB) + qbg) * p.NW + seg / 32 + w] : 0u;
+        }
+        __syncthreads();
+        auto process = [&](const uint16_t* buf, int ct, const auto& refill) {
+          // Branch-free: a tile with no approximated block for this query
+          // block (or a query block past the end) has every score at -inf and
+          // adds nothing.
+          const uint64_t approx = live ? tile_approx(s_mask[qg], ct - ct0, r0, r1) : 0ull;
+          centroid_tile<D>(st, buf, ct, approx, tk, qf, col, hh, scale_log2, refill);
+        };
+        tile_stream<D, NT, R>(ring, nct, RangeCursor{ct_lo}, crefill, tile_runs(always, process, process), process,
+                              wave, lane);
+      } else {
+        // Per tile: routing of the tile's 64 blocks for every query block of
+        // the group -- wave w scores blocks 32 (w & 1) + (lane & 31) of query
+        // block w >> 1 over feature half lane >> 5, the halves summed across
+        // the lane pair -- into the LDS bitmask; a barrier publishes the mask;
+        // then the approximated blocks' contributions.
+        auto process = [&](const uint16_t* buf, int ct, const auto& refill) {
+          const int r = fresh(32 * qh + col);  // centroid row inside the tile
+          const int j = kBlock * ct + r;
+          bool sel = false;
+          if (live && j >= seg + r0 && j < seg + r1) {
+            if (p.force == 0) {
+              const int c0 = fresh(hh) * (S::DC / 2);  // first 16-byte chunk of this lane's feature half
+              float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int c = 0; c < S::DC / 2; ++c) {
+                const int cc = c0 + c;
+                const u32x4 x = *reinterpret_cast<const u32x4*>(buf + TL::k_offset(r, cc));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                  const uint32_t w = x[e >> 1];
+                  part[e & 3] = fmaf(s_qm[qg][8 * cc + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)),
+                                     part[e & 3]);
+                }
+              }
+              const float proxy = pair_sum((part[0] + part[1]) + (part[2] + part[3]));
+              sel = proxy > s_cut[qg];
+              if (p.dbg_proxy && hh == 0) p.dbg_proxy[dbg_row + j] = proxy * p.scale;
+            }
+            sel = sel || (p.local_blocks >= 0 && abs(j - qb) <= p.local_blocks) || j < p.kv_sink_blocks ||
+                  qb < p.q_sink_blocks;
+            if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * p.NKB + j] != 0;
+            if (p.dbg_selected && hh == 0) p.dbg_selected[dbg_row + j] = sel ? 1 : 0;
+          }
+          const uint64_t bal = __ballot(sel);
+          if (lane == 0) s_mask[qg][2 * (ct - ct0) + qh] = uint32_t(bal);
+          lds_barrier();  // publishes the mask words
+          // Branch-free: a tile with no approximated block for this query block
+          // (or a query block past the end) has every score at -inf and adds
+          // nothing.
+          const uint64_t approx = live ? tile_approx(s_mask[qg], ct - ct0, r0, r1) : 0ull;
+          centroid_tile<D>(st, buf, ct, approx, tk, qf, col, hh, scale_log2, refill);
+        };
+        tile_stream<D, NT, R>(ring, nct, RangeCursor{ct_lo}, crefill, tile_runs(always, process, process), process,
+                              wave, lane);
+      }
       lds_barrier();  // every wave is done with the ring's centroid tiles
     }
     if (live && p.counts && lt == 0)
@@ -940,6 +967,13 @@ void launch_sol_group(const AttnParams& p, hipStream_t stream) {
 }
 
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
+  // Routing first when its masks go to the routing workspace (beta = -inf
+  // selects every block and needs none; without a workspace the attention
+  // kernel routes tile by tile).
+  if (p.force != 1 && p.mask) {
+    const hipError_t err = launch_route(p, D, stream);
+    if (err != hipSuccess) return err;
+  }
   int g = int64_t(p.B) * p.H * ((p.NQB + 1) / 2) < kSmallLaunchGroups ? 1 : 2;
   if (p.workgroup_form == 1 || p.workgroup_form == 2) g = p.workgroup_form;
   if (D == 128) {

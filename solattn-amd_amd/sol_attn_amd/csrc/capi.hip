@@ -86,6 +86,11 @@ int scratch_on_current_device(void** ptr) {
 
 int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
+// Routing masks of sol_attention_fwd: uint32 [batch, heads, NQB, ceil(NKB / 32)].
+int64_t route_mask_bytes(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads) {
+  return batch * heads * cdiv(query_tokens, SOL_BLOCK) * cdiv(cdiv(key_tokens, SOL_BLOCK), 32) * 4;
+}
+
 // Key-range parts per query-sink tile of the SOL kernel (sol_task).  A
 // query-sink block selects every key block, so its workgroup streams all of
 // them and, in a launch of few workgroups, ends long after the rest.  Split:
@@ -234,7 +239,7 @@ int64_t sol_pair_workspace_size(int64_t batch, int64_t query_tokens, int64_t hea
 int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* query_index,
                      int64_t sequence_length, int64_t batch, int64_t query_tokens,
                      int64_t heads, int64_t head_dim, void* workspace, int32_t* strides,
-                     void* stream) {
+                     float* query_means, void* stream) {
   const int64_t bytes = sol_pair_workspace_size(batch, query_tokens, heads, head_dim);
   if (bytes == 0)
     return fail(SOL_ERR_UNSUPPORTED,
@@ -254,6 +259,7 @@ int sol_pair_strides(const void* q, const int64_t* q_strides, const int64_t* que
   p.means = static_cast<float*>(workspace);
   p.lags = p.means + batch * heads * head_dim * p.NQB;
   p.strides = strides;
+  p.qc = query_means;
   return hip_status(sol::launch_pairing(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
@@ -321,6 +327,15 @@ int64_t sol_split_workspace_size(int64_t batch, int64_t query_tokens, int64_t ke
   return split_bytes(bh, qsb, s, head_dim);
 }
 
+int64_t sol_route_workspace_size(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                                 double beta) {
+  if (!shape_ok(batch, query_tokens, heads, 64) || key_tokens <= 0 || key_tokens >= (int64_t(1) << 30) ||
+      std::isnan(beta))
+    return 0;
+  if (std::isinf(beta) && beta < 0) return 0;  // every block exact: no routing
+  return route_mask_bytes(batch, query_tokens, key_tokens, heads);
+}
+
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t sequence_length, int64_t batch, int64_t query_tokens,
                       int64_t key_tokens,
@@ -328,7 +343,8 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                       const void* tiles, const void* ctiles, const float* key_mean,
                       const float* key_var, const float* key_cov, const uint8_t* protection,
-                      const int32_t* pair_strides, void* split_workspace, double scale, double beta,
+                      const int32_t* pair_strides, void* split_workspace, void* route_workspace,
+                      const float* query_means, double scale, double beta,
                       int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens,
                       void* out, const int64_t* out_index, int32_t* counts,
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
@@ -352,9 +368,12 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: sink token counts must be nonnegative");
   const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
   if (!ctiles || !aligned16(ctiles) || !out || !aligned16(out) || (tiles && !aligned16(tiles)) ||
-      (split_workspace && !aligned16(split_workspace)))
+      (split_workspace && !aligned16(split_workspace)) || (route_workspace && !aligned16(route_workspace)))
     return fail(SOL_ERR_INVALID,
-                "sol_attention_fwd: tiles/ctiles/out/split_workspace must be 16-byte aligned device buffers");
+                "sol_attention_fwd: tiles/ctiles/out/split_workspace/route_workspace must be 16-byte aligned "
+                "device buffers");
+  if (query_means && !route_workspace)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_means are read only with a route_workspace");
   if (!tiles) {
     const int rc = rows_mode_ok("sol_attention_fwd", k, k_strides, v, v_strides, key_lengths, key_tokens);
     if (rc != SOL_OK) return rc;
@@ -407,6 +426,9 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   p.q_sink_blocks = int(sink_blocks(query_sink_tokens));
   p.splits = split_workspace ? sink_splits(batch * heads, nqb, nkb, p.q_sink_blocks, force, head_dim) : 1;
   p.partial = p.splits > 1 ? static_cast<float*>(split_workspace) : nullptr;
+  p.mask = force != 1 ? static_cast<uint32_t*>(route_workspace) : nullptr;
+  p.NW = int(cdiv(nkb, 32));
+  p.qc = query_means;
   return hip_status(sol::launch_sol(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
@@ -527,7 +549,8 @@ int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k
   if (prc != SOL_OK) return prc;
   return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
                            head_dim, k, k_strides, v, v_strides, tiles, ws, mean, var, nullptr, nullptr, nullptr,
-                           split ? ws + off_split : nullptr, scale, beta,
+                           split ? ws + off_split : nullptr, nullptr /* routing in the attention kernel */,
+                           nullptr, scale, beta,
                            local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr, counts, nullptr,
                            nullptr, nullptr, nullptr, nullptr, 0, stream);
 }

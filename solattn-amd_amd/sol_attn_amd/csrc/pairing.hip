@@ -29,7 +29,9 @@ namespace {
 constexpr int kMeanThreads = 256;  // four waves
 constexpr int kMeanChunk = 16;     // query blocks per workgroup
 
-// Normalised query-block means, m[((b H + h) D + d) NQB + i] (lag-major rows
+// Query-block means: with p.qc, the FP32 means themselves, qc[((b H + h) NQB
+// + i) D + d] (the routing kernel's Qc); and the normalised means,
+// m[((b H + h) D + d) NQB + i] (lag-major rows
 // so that the lag kernel reads one feature of one head contiguously).  One
 // workgroup per (batch entry, head, 16 consecutive query blocks), in the
 // pooling kernel's load shape: each lane holds 16 rows x 16 bytes of one
@@ -67,15 +69,23 @@ __global__ __launch_bounds__(kMeanThreads) void qblock_means_kernel(PairParams p
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const uint32_t w = x[r][e >> 1];
-          s[e] += bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu));
+          s[e] = __fadd_rn(s[e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)));
         }
     }
+    // The four 16-row quarter sums fold in order, ((q0 + q1) + q2) + q3:
+    // torch's cascade order for a 64-row block, so the FP32 mean equals the
+    // reference oracle's `_means` (reference.py:13-15) bit for bit.
     float n2 = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      s[e] += __shfl(s[e], lane + DC) + __shfl(s[e], lane + 2 * DC) + __shfl(s[e], lane + 3 * DC);
-      s[e] = qlen > 0 ? s[e] / float(qlen) : 0.f;
+      const float c1 = __shfl(s[e], lane + DC), c2 = __shfl(s[e], lane + 2 * DC), c3 = __shfl(s[e], lane + 3 * DC);
+      s[e] = qlen > 0 ? __fdiv_rn(__fadd_rn(__fadd_rn(__fadd_rn(s[e], c1), c2), c3), float(qlen)) : 0.f;
       n2 += s[e] * s[e];
+    }
+    if (p.qc && r4 == 0 && i < p.NQB) {
+      float* dst = p.qc + (int64_t(bh) * p.NQB + i) * D + 8 * dc;
+      *reinterpret_cast<f32x4*>(dst) = f32x4{s[0], s[1], s[2], s[3]};
+      *reinterpret_cast<f32x4*>(dst + 4) = f32x4{s[4], s[5], s[6], s[7]};
     }
     // The DC lanes of quarter 0 of a block are consecutive and DC-aligned.
 #pragma unroll

@@ -47,6 +47,7 @@ constexpr int kMaxPairBlocks = 8192;   // query blocks per (entry, head) the lag
 
 struct PairParams {
   TokenRows q;
+  float* qc;         // [B, H, NQB, D] FP32 query-block means (cascade order), or null
   float* means;      // [B, H, D, NQB] normalised query-block means
   float* lags;       // [B, H, D, kMaxLag] per-feature lag sums
   int32_t* strides;  // [B, H] chosen pairing stride
@@ -82,6 +83,10 @@ struct AttnParams {
                        // sol_attention_kernel
   int splits;          // key-range parts per front (query-sink) tile, >= 1 (sol_task)
   float* partial;      // their partial states when splits > 1: rows [B H][front][G 64][D + 4]
+  uint32_t* mask;      // [B, H, NQB, NW] routing decisions (route_kernel), bit j of word w = key block 32 w + j;
+                       // null: the attention kernel routes tile by tile
+  int NW;              // ceil(NKB / 32)
+  const float* qc;     // [B, H, NQB, D] FP32 query-block means for route_kernel, or null (formed from Q)
 };
 
 // Indexed-window protection (plan.hip).
@@ -107,6 +112,7 @@ struct QuantParams {
 
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream);
 hipError_t launch_quantize_keys(const QuantParams& p, int D, hipStream_t stream);
+hipError_t launch_route(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_dense(const AttnParams& p, int D, hipStream_t stream);
 hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream);

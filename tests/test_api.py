@@ -145,7 +145,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == _native.ABI_VERSION == 9
+    assert native.sol_abi_version() == _native.ABI_VERSION == 10
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -169,27 +169,33 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     assert rc == -1 and b"scale" in native.sol_last_error()
     attn = lambda index, n, form: native.sol_attention_fwd(  # noqa: E731
         fake, strides, index, n, 1, 193, 317, None, 2, 64, None, None, None, None, fake, fake, fake, fake,
-        None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, form, None)
+        None, None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, form, None)
     rc = native.sol_attention_fwd(fake, strides, None, 0, 1, 193, 317, None, 2, 64, None, None, None, None,
-                                  fake, fake, None, None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake,
+                                  fake, fake, None, None, None, None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake,
                                   None, None, None, None, None, None, None, 0, None)
     assert rc == -1 and b"key_mean" in native.sol_last_error()
+    rc = native.sol_attention_fwd(fake, strides, None, 0, 1, 193, 317, None, 2, 64, None, None, None, None,
+                                  fake, fake, fake, fake, None, None, None, None, None, fake, 0.125, 1.0, 1, 0, 0,
+                                  fake, None, None, None, None, None, None, None, 0, None)
+    assert rc == -1 and b"query_means" in native.sol_last_error()
+    assert native.sol_route_workspace_size(1, 193, 317, 2, float("-inf")) == 0
+    assert native.sol_route_workspace_size(2, 193, 317, 3, 1.0) == 2 * 3 * 4 * 1 * 4
     assert attn(None, 0, 3) == -1 and b"workgroup_form" in native.sol_last_error()
     assert attn(fake, 0, 0) == -1 and b"sequence_length" in native.sol_last_error()
     # Without tiles the keys must qualify for rows mode.
     rows = lambda nk, lengths: native.sol_attention_fwd(  # noqa: E731
         fake, strides, None, 0, 1, 193, nk, lengths, 2, 64, fake, strides, fake, strides, None, fake,
-        fake, fake, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None,
+        fake, fake, None, None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None,
         0, None)
     assert rows(63, None) == -1 and b"without tiles" in native.sol_last_error()
     assert rows(317, fake) == -1 and b"without tiles" in native.sol_last_error()
     rc = native.sol_quantize_keys(fake, strides, None, None, 0, 1, 40, 2, 64, 1, fake, fake, None)
     assert rc == -1 and b"rows_mode" in native.sol_last_error()
-    rc = native.sol_pair_strides(fake, strides, None, 0, 1, 192, 2, 64, fake, fake, None)
+    rc = native.sol_pair_strides(fake, strides, None, 0, 1, 192, 2, 64, fake, fake, None, None)
     assert rc == -2 and b"4 .. 8192 query blocks" in native.sol_last_error()
-    rc = native.sol_pair_strides(fake, strides, None, 0, 1, 193, 2, 64, None, fake, None)
+    rc = native.sol_pair_strides(fake, strides, None, 0, 1, 193, 2, 64, None, fake, None, None)
     assert rc == -1 and b"workspace" in native.sol_last_error()
-    rc = native.sol_pair_strides(fake, strides, fake, 0, 1, 193, 2, 64, fake, fake, None)
+    rc = native.sol_pair_strides(fake, strides, fake, 0, 1, 193, 2, 64, fake, fake, None, None)
     assert rc == -1 and b"sequence_length" in native.sol_last_error()
     bad = (ctypes.c_int64 * 3)(64 * 2 * 317, 127, 64)
     rc = native.sol_pool_kv(fake, bad, fake, strides, None, None, 0, 1, 317, 2, 64, fake, fake,

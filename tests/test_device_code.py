@@ -4,7 +4,7 @@ The key-block DMA (``dma16`` in ``csrc/attn_common.h``) writes M0 in inline
 assembly and declares it clobbered, which hipcc does not honour for a
 reserved register.  That is only sound while no other instruction of these
 kernels touches M0, so the assembly is checked: every write of M0 is the
-DMA's own ``s_mov_b32 m0, sN`` / ``s_nop 0`` / ``global_load_lds_dwordx4``
+DMA's own ``s_mov_b32 m0, <SGPR>`` / ``s_nop 0`` / ``global_load_lds_dwordx4``
 sequence, and nothing else names M0.
 """
 
@@ -33,7 +33,8 @@ def test_only_the_key_block_dma_uses_m0(tmp_path):
     for i, line in enumerate(code):
         if not re.search(r"\bm0\b", line):
             continue
-        assert re.fullmatch(r"s_mov_b32 m0, s\d+", line), f"unexpected use of M0: {line!r}"
+        # The asm statement's scalar operand: any SGPR (vcc_lo/vcc_hi are SGPRs too).
+        assert re.fullmatch(r"s_mov_b32 m0, (s\d+|vcc_lo|vcc_hi)", line), f"unexpected use of M0: {line!r}"
         assert code[i + 1] == "s_nop 0" and code[i + 2].startswith("global_load_lds_dwordx4"), \
             f"M0 write not followed by the DMA: {code[i:i + 3]!r}"
         writes += 1

@@ -87,8 +87,8 @@ def test_pairing_never_changes_results(beta, d, monkeypatch):
     # Forced strides (including ones past the query blocks) are valid pairings too.
     pooled = _native.pool_kv(k, v, moments=not math.isinf(beta))
     for s in (1, 2, 5, 9, 40, 1 << 30):
-        monkeypatch.setattr(_native, "pair_strides", lambda q, rows=None, s=s, **kw: torch.full(
-            (1, 2), s, device=q.device, dtype=torch.int32))
+        monkeypatch.setattr(_native, "_pairing", lambda q, rows=None, stream=None, s=s: (torch.full(
+            (1, 2), s, device=q.device, dtype=torch.int32), None))
         monkeypatch.setattr(_native, "PAIRING", True)
         out, counts, _ = _native.attend(q, pooled, d ** -0.5, beta, 1, 64, 0)
         assert torch.equal(out, ref), s
