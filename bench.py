@@ -44,12 +44,12 @@ PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 METRIC = "ms/call & dense-equiv TFLOP/s at 84,672 tok H24 D128 BF16; density; err vs oracle"
 
-# Inputs are drawn from ONE generator per workload, seed 0, in the order Q, K,
-# V (block-smooth: each tensor's block centres, then its noise).  The
-# block-smooth and random fixtures use a CPU generator in FP32 and are cast to
-# BF16 before the copy to the GPU, so the oracle and the kernels see the same
-# bits; the 84,672-token field is generated on the GPU (its CPU generation
-# takes about a minute) and copied back for the oracle.
+# Inputs are drawn from ONE CPU generator per workload (torch.Generator, seed
+# 0), in FP32, in the order Q, K, V (block-smooth: each tensor's block
+# centres, then its noise; the smooth field: each tensor's grid, then its
+# noise), cast to BF16 on the CPU and then copied to the GPU, so the oracle
+# and the kernels see the same bits and every input can be reproduced
+# without a GPU.
 WORKLOADS = {
     "videodit-84672": dict(batch=1, frames=21, height=48, width=84, heads=24, head_dim=128,
                            beta=1.0, kv_sink_tokens=128, query_sink_tokens=128, local_blocks=1,
@@ -94,9 +94,9 @@ def block_smooth(gen, batch, tokens, heads, dim, noise=0.1):
 def make_inputs(cfg, device):
     """Q, K, V of a workload on `device` (see WORKLOADS for the generators)."""
     if cfg["fixture"] == "smooth-field":
-        gen = torch.Generator(device=device).manual_seed(cfg["seed"])
+        gen = torch.Generator().manual_seed(cfg["seed"])
         return [smooth_field(gen, cfg["frames"], cfg["height"], cfg["width"], cfg["heads"],
-                             cfg["head_dim"], device) for _ in range(3)]
+                             cfg["head_dim"], torch.device("cpu")).to(device) for _ in range(3)]
     gen = torch.Generator().manual_seed(cfg["seed"])
     b, h, d = cfg["batch"], cfg["heads"], cfg["head_dim"]
     tq = cfg["tokens"]
@@ -420,12 +420,16 @@ def config_record(name, cfg, beta, q, k, v):
             "heads": q.shape[2], "head_dim": q.shape[3], "beta": beta,
             "kv_sink_tokens": cfg["kv_sink_tokens"], "query_sink_tokens": cfg["query_sink_tokens"],
             "local_blocks": cfg["local_blocks"], "fixture": cfg["fixture"], "seed": cfg["seed"],
+            "generator": "torch.Generator('cpu'), FP32 draws in the order Q, K, V, cast to BF16, then copied",
             "q_head_stride_view": cfg.get("q_head_stride", 1) != 1}
 
 
-def measure(name, cfg, beta, args, dev, headline):
+def measure(name, cfg, beta, args, dev, headline, experiments=True):
     """One JSON record: the all-in call, its kernels, the dense control, the
-    roofline of the attention kernel and pooling, parity and the CPU oracle."""
+    roofline of the attention kernel and pooling, parity (every routing
+    decision, and outputs on sampled query blocks) and the CPU oracle.
+    ``experiments=False`` skips the INT8-QK experiment (configuration records
+    embedded in the headline line)."""
     from sol_attn_amd import _native, dense_attention, sol_attention
 
     q, k, v = make_inputs(cfg, dev)
@@ -448,7 +452,9 @@ def measure(name, cfg, beta, args, dev, headline):
         out = step()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
-    call_ms = event_ms(step, args.steps)
+    # HIP events on the launch stream, the timer the dense control gets too
+    # (short calls: more repetitions).
+    call_ms = event_ms(step, args.steps if headline else max(args.steps, 50), warm=not headline)
 
     # Per-kernel breakdown with HIP events on the launch stream.
     with torch.no_grad():
@@ -461,7 +467,7 @@ def measure(name, cfg, beta, args, dev, headline):
                                               cfg["kv_sink_tokens"], cfg["query_sink_tokens"], debug=True)
         # Small configurations: more repetitions and one warm call (their
         # calls take tens of microseconds).
-        dense_ms = event_ms(lambda: dense_attention(q, k, v), args.dense_reps if headline else max(args.dense_reps, 20),
+        dense_ms = event_ms(lambda: dense_attention(q, k, v), args.dense_reps if headline else max(args.steps, 50),
                             warm=not headline)
     torch.cuda.synchronize()
     deterministic = bool(torch.equal(ref_out, out))
@@ -486,6 +492,7 @@ def measure(name, cfg, beta, args, dev, headline):
         "dense_hip_ms": dense_ms,
         "dense_hip_tflops": dense_flops / (dense_ms * 1e-3) / 1e12,
         "speedup_vs_dense_hip": dense_ms / wall_ms,
+        "speedup_vs_dense_hip_events": dense_ms / call_ms,
         "roofline": {"bound": "mfma", "achieved": attn_tflops, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": attn_tflops / PEAK_BF16_TFLOPS,
                      "traffic": traffic["traffic_bytes"] if traffic else None,
@@ -506,7 +513,7 @@ def measure(name, cfg, beta, args, dev, headline):
     }
     if headline and finite and not args.no_threshold_experiment:
         result["threshold_experiment"] = threshold_experiment(q, k, v, kw, out, density)
-    if finite and not args.no_qk_int8 and (headline or (name.startswith("selfattn-4096") and beta == 1.0)):
+    if finite and experiments and not args.no_qk_int8 and (headline or (name.startswith("selfattn-4096") and beta == 1.0)):
         with torch.no_grad():
             _, bf16_counts = _native.launch_sol(q, k, v, scale, beta, cfg["local_blocks"], cfg["kv_sink_tokens"],
                                                 cfg["query_sink_tokens"], True)
@@ -525,8 +532,39 @@ def measure(name, cfg, beta, args, dev, headline):
             "implementation": CPU_BASELINE_KIND,
             "ms_per_call" if whole else "ms_per_call_extrapolated": t_full * 1e3,
             "sample": sample_txt, "host": host}
+        # Every routing decision of the call (float64 Qc . Kc_j, the stated band).
+        from oracle import sol_oracle as orc
+        t0 = time.perf_counter()
+        parity["routing_every_decision"] = orc.routing_check(
+            q.cpu(), k.cpu(), dbg["selected"].cpu(), beta=beta, scale=scale, local_blocks=cfg["local_blocks"],
+            kv_sink_tokens=cfg["kv_sink_tokens"], query_sink_tokens=cfg["query_sink_tokens"])
+        parity["routing_every_decision"]["seconds"] = time.perf_counter() - t0
+        parity["routing_every_decision"]["band"] = "|proxy - cutoff| <= 1e-5 max(|cutoff|, scale |Qc| |Kc_j|)"
         result["parity_vs_oracle"] = parity
     return result
+
+
+def config_summary(rec):
+    """The per-configuration fields carried in the headline line (one timer,
+    HIP events, for the SOL call and the dense control)."""
+    c = rec["config"]
+    out = {"shape": f"B{c['batch']} Tq{c['query_tokens']} Tk{c['key_tokens']} H{c['heads']} D{c['head_dim']}",
+           "fixture": c["fixture"], "beta": c["beta"], "density": rec["density"],
+           "sol_ms": rec["sol_ms_per_call_events"], "dense_ms": rec["dense_hip_ms"],
+           "speedup_vs_dense": rec["speedup_vs_dense_hip_events"],
+           "attention_ms": rec["kernels_ms"]["sol_attention"], "pool_ms": rec["kernels_ms"]["pool_kv"],
+           "dense_equiv_tflops": rec["value"] * rec["ms_per_step"] / rec["sol_ms_per_call_events"]}
+    par = rec.get("parity_vs_oracle")
+    if par:
+        r = par["routing_every_decision"]
+        out.update({"routing_decisions": r["decisions"], "routing_outside_band": r["outside_band"],
+                    "routing_in_band_mismatches": r["mismatches"], "max_abs_vs_oracle": par["max_abs"],
+                    "rel_l2_vs_oracle": par["rel_l2"], "counts_equal": par["counts_equal"],
+                    "oracle_sampled_query_blocks": par["sampled_query_blocks"]})
+        cpu = rec["cpu_baseline"]
+        out["cpu_oracle_ms"] = cpu.get("ms_per_call", cpu.get("ms_per_call_extrapolated"))
+        out["cpu_oracle_ms_kind"] = "whole call" if "ms_per_call" in cpu else "extrapolated from the sample"
+    return out
 
 
 def main():
@@ -548,6 +586,8 @@ def main():
                     help="skip the full- vs diagonal-covariance threshold comparison")
     ap.add_argument("--no-qk-int8", action="store_true",
                     help="skip the INT8-QK experiment (run at beta=1 on the headline and 4,096-token workloads)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-configuration records (C1-C3) in the headline line")
     ap.add_argument("--copy-gib", type=float, default=0.0,
                     help="also run a device copy of this many GiB (HBM counter calibration)")
     args = ap.parse_args()
@@ -567,6 +607,16 @@ def main():
     cfg = WORKLOADS[args.workload]
     beta = cfg["beta"] if args.beta is None else args.beta
     result = measure(args.workload, cfg, beta, args, dev, headline=True)
+    if not args.no_configs:
+        # The survey's other configurations, each with its own seed-0 inputs.
+        configs = {}
+        for name, betas in SWEEP:
+            for b in betas:
+                rec = measure(name, WORKLOADS[name], b, args, dev, headline=False, experiments=False)
+                configs[f"{name} beta={b}"] = config_summary(rec)
+                print(f"config {name} beta={b}: {configs[f'{name} beta={b}']['sol_ms']:.4f} ms", file=sys.stderr,
+                      flush=True)
+        result["configs"] = configs
     if args.copy_gib > 0:
         # One elementwise kernel that reads and writes exactly copy_gib GiB each.
         src = torch.empty(int(args.copy_gib * (1 << 30)) // 4, device=dev, dtype=torch.float32)

@@ -288,6 +288,83 @@ def route(q: np.ndarray, kc: np.ndarray, cut: np.ndarray, *, beta: float, scale:
     return selected, proxy
 
 
+def routing_check(q, k, kernel_selected, *, beta: float, scale: Optional[float] = None,
+                  local_blocks: int = 1, kv_sink_tokens: int = 0, query_sink_tokens: int = 0,
+                  protected_blocks=None, threshold_estimator: str = "diagonal_covariance",
+                  band: float = 1e-5) -> dict:
+    """Every (batch, query block, head, key block) decision of a kernel against
+    the oracle's, at any size.
+
+    The proxy ``scale * mean_r (Q_r . Kc_j)`` (``reference.py:39``) equals
+    ``scale * Qc . Kc_j`` in exact arithmetic (``Qc`` the query block's mean),
+    so it is formed as one float64 product per head, ``Qc Kc^T``, from the
+    oracle's bit-exact FP32 ``Qc`` and BF16 ``Kc``; the cutoff
+    (``reference.py:29-30``) likewise in float64 from the oracle's FP32
+    moments.  Decisions: ``proxy > cutoff`` (strict), forced for beta = +-inf,
+    OR the local band, sinks and plan protection (``reference.py:40-51``).
+    A kernel decision may differ only where
+    ``|proxy - cutoff| <= band * max(|cutoff|, scale |Qc| |Kc_j|)`` (the
+    magnitudes an FP32 evaluation rounds against).  ``kernel_selected``:
+    bool ``[B, NQB, H, NKB]``.  Returns counts: ``decisions``, ``mismatches``,
+    ``outside_band`` (must be 0), ``in_band`` (decisions inside the band) and
+    ``max_rel_gap`` (largest ``|proxy - cutoff|`` over the band's scale among
+    the mismatches; at most 1 when none lies outside).
+    """
+    q, k = _as_f32(q), _as_f32(k)
+    ksel = _as_bool(kernel_selected)
+    d = q.shape[-1]
+    scale = d ** -0.5 if scale is None else float(scale)
+    qm = block_means(q, round_bf16=False)
+    kc = block_means(k, round_bf16=True)
+    mean, var = key_moments(kc)
+    b, nqb, h, _ = qm.shape
+    nkb = kc.shape[1]
+    prot_static = _protection_mask(nqb, nkb, local_blocks, kv_sink_tokens, query_sink_tokens)
+    prot = None if protected_blocks is None else _as_bool(protected_blocks)
+    cov = key_covariance(kc) if threshold_estimator == "full_covariance" else None
+    res = dict(decisions=0, mismatches=0, outside_band=0, in_band=0, max_rel_gap=0.0)
+    for bi in range(b):
+        for hi in range(h):
+            q64 = qm[bi, :, hi].astype(np.float64)                    # [NQB, D]
+            k64 = kc[bi, :, hi].astype(np.float64)                    # [NKB, D]
+            if beta == -math.inf:
+                sel = np.ones((nqb, nkb), bool)
+                gap = rel = None
+            elif beta == math.inf:
+                sel = np.zeros((nqb, nkb), bool)
+                gap = rel = None
+            else:
+                mu = q64 @ mean[bi, hi].astype(np.float64)
+                if cov is None:
+                    quad = (q64 * q64) @ var[bi, hi].astype(np.float64)
+                else:
+                    quad = np.maximum(np.einsum("qd,de,qe->q", q64, cov[bi, hi].astype(np.float64), q64), 0.0)
+                cut = scale * (mu + beta * np.sqrt(quad))                 # [NQB]
+                proxy = scale * (q64 @ k64.T)                             # [NQB, NKB]
+                sel = proxy > cut[:, None]
+                width = band * np.maximum(np.abs(cut)[:, None],
+                                          scale * np.linalg.norm(q64, axis=1)[:, None]
+                                          * np.linalg.norm(k64, axis=1)[None, :])
+                gap = np.abs(proxy - cut[:, None])
+                rel = gap / np.maximum(width, np.finfo(np.float64).tiny)
+            sel |= prot_static
+            if prot is not None:
+                sel |= prot[bi]
+            got = ksel[bi, :, hi]
+            diff = got != sel
+            res["decisions"] += sel.size
+            res["mismatches"] += int(diff.sum())
+            if rel is None:
+                res["outside_band"] += int(diff.sum())
+            else:
+                inside = rel <= 1.0
+                res["in_band"] += int(inside.sum())
+                res["outside_band"] += int((diff & ~inside).sum())
+                if diff.any():
+                    res["max_rel_gap"] = max(res["max_rel_gap"], float(rel[diff].max()))
+    return res
+
+
 # ----------------------------------------------------------------------------
 # Attention
 # ----------------------------------------------------------------------------

@@ -23,7 +23,8 @@ import bench
 from oracle.sol_oracle import sol_oracle
 from sol_attn_amd import IndexedPlan, dense_attention, sol_attention, sol_attention_indexed
 from sol_testlib import HAS_GPU, assert_close
-from test_kernels import check_routing
+from oracle import sol_oracle as orc
+from test_kernels import check_routing, run_debug
 
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not HAS_GPU, reason="AMD ROCm GPU required")]
 
@@ -44,6 +45,21 @@ def test_full_size_sampled_parity(field):
                                 kv_sink=CFG["kv_sink_tokens"], q_sink=CFG["query_sink_tokens"],
                                 query_blocks=sample)
     assert_close(got, ref)
+
+
+def test_full_size_routing_every_decision(field):
+    # All 1,323 x 1,323 x 24 = 42.0M (query block, key block, head) decisions
+    # against the oracle's (float64 Qc . Kc_j): none outside the routing band.
+    q, k, v = field
+    _, _, dbg = run_debug(q, k, v, CFG["beta"], local=CFG["local_blocks"], kv_sink=CFG["kv_sink_tokens"],
+                          q_sink=CFG["query_sink_tokens"])
+    sel = dbg["selected"].cpu()
+    del dbg
+    res = orc.routing_check(q.cpu(), k.cpu(), sel, beta=CFG["beta"], local_blocks=CFG["local_blocks"],
+                            kv_sink_tokens=CFG["kv_sink_tokens"], query_sink_tokens=CFG["query_sink_tokens"])
+    print(f"routing every decision (84,672 tokens): {res}", flush=True)
+    assert res["decisions"] == 1323 * 1323 * 24
+    assert res["outside_band"] == 0
 
 
 def test_full_size_properties(field):

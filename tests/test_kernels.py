@@ -232,6 +232,26 @@ def test_c2_shape_routing_and_output(beta, kind):
     assert_close(actual, ref)
 
 
+@pytest.mark.parametrize("beta", [-math.inf, 0.0, 1.0, math.inf])
+@pytest.mark.parametrize("name", ["selfattn-4096-smooth", "selfattn-4096-random", "crossattn-4096x10000-random"])
+def test_routing_every_decision(name, beta):
+    # Every (query block, key block, head) decision of the configuration's
+    # call against the oracle's (float64 Qc . Kc_j): none outside the band.
+    cfg, q, k, v = workload(name)
+    if name.startswith("cross") and beta != 1.0:
+        pytest.skip("the cross-attention configuration runs at beta 1")
+    kw = dict(local_blocks=cfg["local_blocks"], kv_sink_tokens=cfg["kv_sink_tokens"],
+              query_sink_tokens=cfg["query_sink_tokens"])
+    _, counts, dbg = run_debug(q, k, v, beta, local=kw["local_blocks"], kv_sink=kw["kv_sink_tokens"],
+                               q_sink=kw["query_sink_tokens"])
+    res = orc.routing_check(q.cpu(), k.cpu(), dbg["selected"].cpu(), beta=beta, **kw)
+    print(f"routing every decision {name} beta={beta}: {res}", flush=True)
+    assert res["decisions"] == dbg["selected"].numel()
+    assert res["outside_band"] == 0
+    assert res["mismatches"] <= MAX_BAND_MISMATCH_RATE * res["decisions"]
+    np.testing.assert_array_equal(counts.cpu().numpy(), dbg["selected"].sum(-1).cpu().numpy())
+
+
 def test_c3_ragged_cross_attention_strided_query():
     # B=1, H=24, D=128, Tq=4096, Tk=10000, Q head-strided view, random, seed 0;
     # beta 1, kv sink 64, q sink 0, local 0.

@@ -393,3 +393,58 @@ def test_quantised_qk_accuracy_against_bf16_control():
            for name, f in (("fp8", fp8), ("int8", int8_rows))}
     assert 0.02 < err["fp8"] < 0.06, err
     assert 0.004 < err["int8"] < 0.012, err
+
+
+# --- routing_check: every decision at any size (float64 Qc . Kc_j) ------------
+
+@pytest.mark.parametrize("name", sorted(GOLDEN_A))
+def test_routing_check_agrees_with_reference_routing(name):
+    # The reference's own routing (per-row products, mean; `route`, whose
+    # counts equal the reference oracle's golden counts) passes the check
+    # with no decision outside the band, on every golden fixture.
+    z = _golden()
+    q, k, v = (orc.bf16_bits_to_f32(z["A_" + n]) for n in "qkv")
+    kw = dict(GOLDEN_A[name])
+    _, counts, info = orc.sol_oracle(q, k, v, **kw)
+    np.testing.assert_array_equal(counts, z[f"A_{name}_counts"])
+    beta = kw.pop("beta")
+    res = orc.routing_check(q, k, info["selected"], beta=beta, **kw)
+    assert res["outside_band"] == 0 and res["decisions"] == info["selected"].size
+    assert res["mismatches"] == 0  # no fixture decision sits inside the 1e-5 band
+
+
+def test_routing_check_protected_plan_and_full_covariance():
+    z = _golden()
+    q, k, v = (orc.bf16_bits_to_f32(z["C_" + n]) for n in "qkv")
+    _, counts, info = orc.sol_oracle(q, k, v, beta=1.0, local_blocks=-1, protected_blocks=z["C_prot"])
+    np.testing.assert_array_equal(counts, z["C_b1_counts"])
+    res = orc.routing_check(q, k, info["selected"], beta=1.0, local_blocks=-1, protected_blocks=z["C_prot"])
+    assert res["outside_band"] == 0 and res["mismatches"] == 0
+    _, _, full = orc.sol_oracle(q, k, v, beta=1.0, threshold_estimator="full_covariance")
+    res = orc.routing_check(q, k, full["selected"], beta=1.0, threshold_estimator="full_covariance")
+    assert res["outside_band"] == 0
+
+
+def test_routing_check_flags_planted_mistakes():
+    z = _golden()
+    q, k, v = (orc.bf16_bits_to_f32(z["A_" + n]) for n in "qkv")
+    _, _, info = orc.sol_oracle(q, k, v, beta=1.0, local_blocks=0)
+    sel = info["selected"]
+    # The decision farthest from its cutoff, flipped: outside the band.
+    gap = np.abs(info["proxy"] - info["cutoff"][..., None])
+    gap[sel & ~(info["proxy"] > info["cutoff"][..., None])] = -1.0  # protected blocks aside
+    far = np.unravel_index(np.argmax(gap), gap.shape)
+    bad = sel.copy()
+    bad[far] = ~bad[far]
+    res = orc.routing_check(q, k, bad, beta=1.0, local_blocks=0)
+    assert res["outside_band"] == 1 and res["mismatches"] == 1 and res["max_rel_gap"] > 1.0
+    # A protected block left unselected, and forced routing: exact agreement is required.
+    bad = sel.copy()
+    bad[0, 0, 0, 0] = False                     # the local band always holds (qb 0, kb 0)
+    assert orc.routing_check(q, k, bad, beta=1.0, local_blocks=0)["outside_band"] == 1
+    _, _, inf = orc.sol_oracle(q, k, v, beta=math.inf, kv_sink_tokens=65, local_blocks=0)
+    bad = inf["selected"].copy()
+    bad[0, -1, 0, -1] = ~bad[0, -1, 0, -1]
+    assert orc.routing_check(q, k, inf["selected"], beta=math.inf, kv_sink_tokens=65,
+                             local_blocks=0)["outside_band"] == 0
+    assert orc.routing_check(q, k, bad, beta=math.inf, kv_sink_tokens=65, local_blocks=0)["outside_band"] == 1
