@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 10
+#define SOL_ABI_VERSION 11
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_TOKENS (1ll << 25) /* key_tokens of one pooling call (2^19 key blocks) */
 
@@ -267,13 +267,24 @@ int sol_plan_protection(const int64_t* rows, const int64_t* keys, const int32_t*
  * tiles: NULL when the keys qualify for rows mode (key_tokens >= 64, token
  * strides below 2^24 elements; see sol_attention_fwd), else a workspace of
  * sol_pool_sizes()[1] bytes (filled here).
- * out: contiguous BF16 [batch, query_tokens, heads, head_dim]. */
+ * query_index: NULL, or int64 [batch, query_tokens] token rows of a
+ * [sequence_length, heads, head_dim] Q (its token and head strides; the batch
+ * stride is ignored), clamped into the sequence -- the gathered queries of
+ * `out[rows] = dense(q[rows], k, v)` (integrations/vdn.py:57-61, the
+ * anchor-row and global queries of a window adapter).
+ * out: contiguous BF16 [batch, query_tokens, heads, head_dim], or with
+ * out_index (int64 [batch, query_tokens]) a contiguous BF16
+ * [sequence_length, heads, head_dim] whose row out_index[b, t] receives query
+ * (b, t); entries outside [0, sequence_length) are not stored.  Keys are the
+ * K / V rows as given (one contiguous token range per call: pass that
+ * range's first row). */
 int sol_dense_fwd(const void* q, const int64_t* q_strides,
+                  const int64_t* query_index, int64_t sequence_length,
                   const void* k, const int64_t* k_strides,
                   const void* v, const int64_t* v_strides,
                   int64_t batch, int64_t query_tokens, int64_t key_tokens,
                   int64_t heads, int64_t head_dim, double scale,
-                  void* tiles, void* out, void* stream);
+                  void* tiles, void* out, const int64_t* out_index, void* stream);
 
 /* All-in SOL attention that allocates nothing: sol_pool_kv followed by
  * sol_attention_fwd (BTHD inputs; no index, plan protection, covariance or
@@ -290,10 +301,20 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides,
  * and V (rows mode), except for fewer than 64 keys or token strides of 2^24
  * elements or more, where the block tiles (4 * head_dim bytes per key token
  * and head) join them, and the split workspace when the problem is split
- * (sol_split_workspace_size); routing runs inside the attention kernel.  Problems needing more than SOL_NOALLOC_SCRATCH_BYTES
- * (128 MiB) return SOL_ERR_UNSUPPORTED before any GPU work.  Every call on
- * one GPU shares that GPU's array: calls that overlap on one GPU (different
- * streams or threads) race and must be serialised by the caller. */
+ * (sol_split_workspace_size); routing runs inside the attention kernel.
+ * Problems needing more than SOL_NOALLOC_SCRATCH_BYTES (128 MiB), and
+ * arguments sol_attention_fwd would reject, return an error before any GPU
+ * work.  Every call on one GPU shares that GPU's array: calls that overlap on
+ * one GPU (different streams or threads) race and must be serialised by the
+ * caller.  The array belongs to the library's device code object: it holds
+ * 128 MiB on every GPU where the library's kernels are loaded (from the first
+ * call on that GPU until the process ends), whether or not this entry point
+ * is ever called.  Some attention kernel
+ * variants (head_dim 128) keep a few values in per-lane private memory
+ * (register spills); the HIP runtime provides that memory per queue and may
+ * size it at the first launch of such a kernel on a queue, which is the
+ * runtime's allocation, not this library's -- a caller that must not see
+ * one makes any SOL call on the queue beforehand. */
 int sol_attention_noalloc(const void* q, const int64_t* q_strides,
                           const void* k, const int64_t* k_strides,
                           const void* v, const int64_t* v_strides,

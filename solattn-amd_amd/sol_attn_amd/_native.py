@@ -13,11 +13,12 @@ import ctypes
 import functools
 import math
 import os
+import threading
 
 import torch
 
 BLOCK = 64
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -44,8 +45,8 @@ _SIGNATURES = {
                            _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                            _dbl, _dbl, _i64, _i64, _i64,
                            _p, _p, _p, _p, _p, _p, _p, _p, _int, _p], ctypes.c_int),
-    "sol_dense_fwd": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
-                       _dbl, _p, _p, _p], ctypes.c_int),
+    "sol_dense_fwd": ([_p, _i64p, _p, _i64, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
+                       _dbl, _p, _p, _p, _p], ctypes.c_int),
     "sol_plan_protection": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _p, _p], ctypes.c_int),
     "sol_key_covariance_workspace_size": ([_i64, _i64, _i64], ctypes.c_int64),
     "sol_key_covariance": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
@@ -304,13 +305,22 @@ def pair_strides(q, rows=None, min_blocks=None, stream=None):
 # caller's stream.  Results are identical either way.
 OVERLAP_PAIRING = True
 _side_streams = {}
+_side_lock = threading.Lock()
 
 
-def _side_stream(device):
-    """One extra stream per device, at the default priority."""
-    side = _side_streams.get(device.index)
+def _side_stream(device, caller):
+    """The side stream of one caller stream (``torch.cuda.Stream``) on
+    ``device``, at the default priority.  Keyed by the caller's stream, so
+    that calls issued concurrently on different streams (other threads, other
+    streams of one thread) do not queue their pairing launches behind each
+    other's."""
+    key = (device.index, caller.cuda_stream)
+    side = _side_streams.get(key)
     if side is None:
-        side = _side_streams[device.index] = torch.cuda.Stream(device=device)
+        with _side_lock:
+            side = _side_streams.get(key)
+            if side is None:
+                side = _side_streams[key] = torch.cuda.Stream(device=device)
     return side
 
 
@@ -467,16 +477,25 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
         pairing = _pair_buffers(q, rows, PAIR_MIN_QUERY_BLOCKS)
         strides = None
         if pairing is not None:
-            main, side = torch.cuda.current_stream(q.device), _side_stream(q.device)
+            main = torch.cuda.current_stream(q.device)
+            side = _side_stream(q.device, main)
             side.wait_stream(main)
-            _pair_launch(pairing[0], rows, pairing[1], pairing[2], pairing[3], side.cuda_stream)
+            try:
+                _pair_launch(pairing[0], rows, pairing[1], pairing[2], pairing[3], side.cuda_stream)
+            except BaseException:
+                main.wait_stream(side)
+                raise
             strides, means = pairing[2], pairing[3]
-    pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths,
-                     stream=stream, views=debug, qk_int8=qk_precision == "int8")
-    if threshold_estimator == "full_covariance" and not math.isinf(beta):
-        key_covariance(pooled, stream)
-    if pairing is not None:
-        main.wait_stream(side)
+    try:
+        pooled = pool_kv(k, v, key_index=keys, moments=not math.isinf(beta), key_lengths=key_lengths,
+                         stream=stream, views=debug, qk_int8=qk_precision == "int8")
+        if threshold_estimator == "full_covariance" and not math.isinf(beta):
+            key_covariance(pooled, stream)
+    finally:
+        # Joined on every path: an error above must not leave the pairing
+        # buffers free for reuse while the side stream still writes them.
+        if pairing is not None:
+            main.wait_stream(side)
     out, counts, dbg = attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection, rows,
                               debug, out, stats, stream, strides=strides, query_means=means)
     del pairing
@@ -506,15 +525,43 @@ def plan_protection(rows, keys, key_lengths, local_tokens, ranges):
     return out.view(torch.bool)
 
 
-def launch_dense(q, k, v, scale):
-    """Dense control (``kernels.py:193-200``): non-causal attention over all keys."""
+def launch_dense(q, k, v, scale, rows=None, out=None):
+    """Dense control (``kernels.py:193-200``): non-causal attention over all keys.
+
+    ``rows`` (int64 ``[W, nq]`` on the Q device): Q is NHD ``[N, H, D]`` and
+    query i of window w is Q row ``rows[w, i]``, gathered inside the kernel;
+    K / V (NHD ``[nk, H, D]``) are the keys every window attends.  With
+    ``out`` (a contiguous BF16 ``[N, H, D]`` tensor) that query's result is
+    stored at ``out[rows[w, i]]`` and ``out`` is returned -- the
+    ``out[rows] = dense(q[rows], k, v)`` of a window adapter's anchor-row and
+    global queries (``integrations/vdn.py:57-61``) in one launch, without
+    gathered copies; otherwise a new ``[W, nq, H, D]`` tensor.
+    """
     lib = library()
     q, k, v = _rows(q), _rows(k), _rows(v)
-    b, nq, h, d = q.shape
+    indexed = rows is not None
+    if indexed:
+        if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+            raise ValueError("indexed dense attention takes NHD Q/K/V")
+        rows = rows.contiguous()
+        w, nq = rows.shape
+        k, v = k.unsqueeze(0), v.unsqueeze(0)
+        b, n, (h, d) = 1, q.shape[0], q.shape[1:]
+        tq = w * nq
+    else:
+        if out is not None:
+            raise ValueError("out= needs rows")
+        b, tq, h, d = q.shape
     nk = k.shape[1]
-    out = torch.empty((b, nq, h, d), device=q.device, dtype=torch.bfloat16)
+    scatter = out is not None
+    if scatter:
+        if out.dtype != torch.bfloat16 or not out.is_contiguous() or out.shape != q.shape or out.device != q.device:
+            raise ValueError("out must be a contiguous BF16 tensor shaped like Q on its device")
+    else:
+        out = torch.empty((w, nq, h, d) if indexed else (b, tq, h, d), device=q.device, dtype=torch.bfloat16)
     tiles = None if rows_mode(k, v) else _tiles(b, h, -(-nk // BLOCK), d, q.device)
-    _check(lib.sol_dense_fwd(q.data_ptr(), _strides(q), k.data_ptr(), _strides(k), v.data_ptr(), _strides(v),
-                             b, nq, nk, h, d, float(scale), _ptr(tiles), out.data_ptr(),
-                             _stream(q.device)))
+    _check(lib.sol_dense_fwd(q.data_ptr(), _strides(q, indexed), _ptr(rows), n if indexed else 0,
+                             k.data_ptr(), _strides(k), v.data_ptr(), _strides(v),
+                             b, tq, nk, h, d, float(scale), _ptr(tiles), out.data_ptr(),
+                             _ptr(rows if scatter else None), _stream(q.device)))
     return out

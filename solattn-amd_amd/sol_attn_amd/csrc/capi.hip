@@ -151,6 +151,35 @@ int rows_mode_ok(const char* who, const void* k, const int64_t* k_strides, const
   return SOL_OK;
 }
 
+// Checks of the attention launch shared by sol_attention_fwd and
+// sol_attention_noalloc (which runs them before its pooling launch, so that a
+// rejected call launches nothing).
+int attention_args_ok(const char* who, const void* q, const int64_t* q_strides, bool indexed, int64_t batch,
+                      int64_t query_tokens, int64_t heads, double scale, double beta, int64_t kv_sink_tokens,
+                      int64_t query_sink_tokens, const void* out) {
+  static thread_local std::string msg;
+  const char* what = nullptr;
+  if (!operand_ok(q, q_strides, indexed))
+    what = ": Q needs 16-byte aligned rows and positive strides";
+  else if (!std::isfinite(scale) || scale <= 0)
+    what = ": scale must be finite and positive";
+  else if (std::isnan(beta))
+    what = ": beta must not be NaN";
+  else if (kv_sink_tokens < 0 || query_sink_tokens < 0)
+    what = ": sink token counts must be nonnegative";
+  else if (!out || !aligned16(out))
+    what = ": out must be a 16-byte aligned device buffer";
+  if (what) {
+    msg = std::string(who) + what;
+    return fail(SOL_ERR_INVALID, msg.c_str());
+  }
+  if (batch * heads * cdiv(query_tokens, SOL_BLOCK) >= (int64_t(1) << 31)) {
+    msg = std::string(who) + ": grid too large";
+    return fail(SOL_ERR_UNSUPPORTED, msg.c_str());
+  }
+  return SOL_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -353,24 +382,20 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
       key_tokens >= (int64_t(1) << 30))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: unsupported shape (head_dim must be 64 or 128)");
-  if (!operand_ok(q, q_strides, query_index != nullptr))
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: Q needs 16-byte aligned rows and positive strides");
+  const int arc = attention_args_ok("sol_attention_fwd", q, q_strides, query_index != nullptr, batch,
+                                    query_tokens, heads, scale, beta, kv_sink_tokens, query_sink_tokens, out);
+  if (arc != SOL_OK) return arc;
   if ((query_index || out_index) && sequence_length <= 0)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_index / out_index need sequence_length > 0");
   if (workgroup_form < 0 || workgroup_form > 2)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: workgroup_form must be 0, 1 or 2");
   if ((qk_int8_tiles == nullptr) != (qk_int8_scales == nullptr) || (qk_int8_tiles && !aligned16(qk_int8_tiles)))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: qk_int8_tiles (16-byte aligned) and qk_int8_scales go together");
-  if (!std::isfinite(scale) || scale <= 0)
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: scale must be finite and positive");
-  if (std::isnan(beta)) return fail(SOL_ERR_INVALID, "sol_attention_fwd: beta must not be NaN");
-  if (kv_sink_tokens < 0 || query_sink_tokens < 0)
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: sink token counts must be nonnegative");
   const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
-  if (!ctiles || !aligned16(ctiles) || !out || !aligned16(out) || (tiles && !aligned16(tiles)) ||
+  if (!ctiles || !aligned16(ctiles) || (tiles && !aligned16(tiles)) ||
       (split_workspace && !aligned16(split_workspace)) || (route_workspace && !aligned16(route_workspace)))
     return fail(SOL_ERR_INVALID,
-                "sol_attention_fwd: tiles/ctiles/out/split_workspace/route_workspace must be 16-byte aligned "
+                "sol_attention_fwd: tiles/ctiles/split_workspace/route_workspace must be 16-byte aligned "
                 "device buffers");
   if (query_means && !route_workspace)
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_means are read only with a route_workspace");
@@ -382,8 +407,6 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
   const int64_t nqb = cdiv(query_tokens, SOL_BLOCK);
-  if (batch * heads * nqb >= (int64_t(1) << 31))
-    return fail(SOL_ERR_UNSUPPORTED, "sol_attention_fwd: grid too large");
   sol::AttnParams p;
   std::memset(&p, 0, sizeof(p));
   p.q = rows_of(q, q_strides, query_index, query_tokens, sequence_length);
@@ -462,15 +485,18 @@ int sol_quantize_keys(const void* k, const int64_t* k_strides, const int64_t* ke
   return hip_status(sol::launch_quantize_keys(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
-int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
-                  const int64_t* k_strides, const void* v, const int64_t* v_strides,
+int sol_dense_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index, int64_t sequence_length,
+                  const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
                   int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
-                  int64_t head_dim, double scale, void* tiles, void* out, void* stream) {
+                  int64_t head_dim, double scale, void* tiles, void* out, const int64_t* out_index,
+                  void* stream) {
   if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
       key_tokens >= (int64_t(1) << 30))
     return fail(SOL_ERR_INVALID, "sol_dense_fwd: unsupported shape (head_dim must be 64 or 128)");
-  if (!operand_ok(q, q_strides, false))
+  if (!operand_ok(q, q_strides, query_index != nullptr))
     return fail(SOL_ERR_INVALID, "sol_dense_fwd: Q needs 16-byte aligned rows and positive strides");
+  if ((query_index || out_index) && sequence_length <= 0)
+    return fail(SOL_ERR_INVALID, "sol_dense_fwd: query_index / out_index need sequence_length > 0");
   if (!std::isfinite(scale) || scale <= 0)
     return fail(SOL_ERR_INVALID, "sol_dense_fwd: scale must be finite and positive");
   if (!out || !aligned16(out)) return fail(SOL_ERR_INVALID, "sol_dense_fwd: out must be 16-byte aligned");
@@ -491,7 +517,9 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides, const void* k,
   }
   sol::AttnParams p;
   std::memset(&p, 0, sizeof(p));
-  p.q = rows_of(q, q_strides, nullptr, query_tokens);
+  p.q = rows_of(q, q_strides, query_index, query_tokens, sequence_length);
+  p.out_index = out_index;
+  p.out_rows = sequence_length;
   p.tiles = rows ? nullptr : static_cast<const uint16_t*>(tiles);
   if (rows) {
     p.k = rows_of(k, k_strides, nullptr, key_tokens);
@@ -517,6 +545,9 @@ int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k
                           int32_t* counts, void* stream) {
   if (!shape_ok(batch, query_tokens, heads, head_dim) || !shape_ok(batch, key_tokens, heads, head_dim))
     return fail(SOL_ERR_INVALID, "sol_attention_noalloc: unsupported shape (head_dim must be 64 or 128)");
+  const int arc = attention_args_ok("sol_attention_noalloc", q, q_strides, false, batch, query_tokens, heads,
+                                    scale, beta, kv_sink_tokens, query_sink_tokens, out);
+  if (arc != SOL_OK) return arc;
   // The sol_pool_kv buffers, 256-byte aligned, in the order sol_pool_sizes lists them.
   int64_t sizes[4];
   if (sol_pool_sizes(batch, key_tokens, heads, head_dim, sizes) != SOL_OK) return SOL_ERR_INVALID;

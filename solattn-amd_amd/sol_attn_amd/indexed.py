@@ -50,6 +50,20 @@ def _distinct(rows):
     return bool(torch.unique(rows).numel() == rows.numel())
 
 
+def _key_range(keys, lengths):
+    """``(start, count)`` when every window's keys are one and the same
+    contiguous token range (keys are strictly increasing over each window's
+    first ``lengths[w]`` entries), else None."""
+    if bool((lengths != lengths[0]).any()):
+        return None
+    count = int(lengths[0])
+    ends = keys[:, [0, count - 1]].cpu()   # one transfer for a device plan
+    start = int(ends[0, 0])
+    if bool((ends[:, 0] != start).any()) or bool((ends[:, 1] - ends[:, 0] != count - 1).any()):
+        return None
+    return start, count
+
+
 def _index_matrix(name, x, sequence_length, device=torch.device("cpu")):
     if (x.device != device or x.dtype != torch.int64 or x.ndim != 2
             or any(n == 0 for n in x.shape)):
@@ -81,6 +95,11 @@ class IndexedPlan:
     # Whether no query row appears in two windows (set by create(); None for a
     # plan built directly, checked on first use with out=).
     rows_distinct: "bool | None" = None
+    # (start, count) when every window's keys are the same contiguous token
+    # range start .. start + count - 1 (set by create(); None otherwise):
+    # beta = -inf then runs the dense kernel on that range of K / V rows,
+    # with no pooling pass and no block tiles.
+    key_range: "tuple | None" = None
 
     @classmethod
     def create(cls, rows, keys, sequence_length, *, protected_ranges=(), local_tokens=64):
@@ -130,12 +149,13 @@ class IndexedPlan:
         rows = rows.clone().contiguous()
         keys = padded.clone().contiguous()
         distinct = _distinct(rows)
+        key_range = _key_range(keys, lengths)
         if dev.type == "cuda":
             from ._native import plan_protection
             key_lengths = lengths.to(torch.int32).to(dev) if ragged else None
             with torch.cuda.device(dev):
                 protection = plan_protection(rows, keys, key_lengths, local_tokens, ranges)
-            return cls(rows, keys, protection, sequence_length, key_lengths, distinct)
+            return cls(rows, keys, protection, sequence_length, key_lengths, distinct, key_range)
         w, nq = rows.shape
         nqb = (nq + BLOCK - 1) // BLOCK
         first = rows[:, ::BLOCK]                                        # [W, NQB]
@@ -146,13 +166,13 @@ class IndexedPlan:
             hi = torch.full((w, 1), b - 1, dtype=torch.int64)
             protection |= _touches(keys, lo, hi, lengths)
         return cls(rows, keys, protection.contiguous(), sequence_length,
-                   lengths.to(torch.int32) if ragged else None, distinct)
+                   lengths.to(torch.int32) if ragged else None, distinct, key_range)
 
     def to(self, device):
         return IndexedPlan(self.rows.to(device), self.keys.to(device),
                            self.protected_blocks.to(device), self.sequence_length,
                            None if self.key_lengths is None else self.key_lengths.to(device),
-                           self.rows_distinct)
+                           self.rows_distinct, self.key_range)
 
 
 def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=False, out=None,
@@ -209,7 +229,20 @@ def sol_attention_indexed(q, k, v, plan, *, beta=1.0, scale=None, return_stats=F
         raise ValueError("beta must not be NaN")
     _threshold_estimator(threshold_estimator)
     _qk_precision(qk_precision)
-    from ._native import launch_sol
+    from ._native import launch_dense, launch_sol
+    if beta == -math.inf and qk_precision == "bf16" and plan.key_range is not None:
+        # Every block exact over one contiguous key range: the dense kernel on
+        # those K / V rows, queries gathered and (with out=) results scattered
+        # inside it -- no pooling pass, no block tiles, no protection needed.
+        start, count = plan.key_range
+        with torch.no_grad(), torch.cuda.device(q.device):
+            result = launch_dense(q, k[start:start + count], v[start:start + count], scale,
+                                  rows=plan.rows, out=out)
+        if return_stats:
+            nkb = (plan.keys.shape[1] + 63) // 64
+            counts = torch.full((b, (nq + 63) // 64, q.shape[1]), nkb, device=q.device, dtype=torch.int32)
+            return result, SolStats(counts, nkb)
+        return result
     with torch.no_grad(), torch.cuda.device(q.device):
         result, counts = launch_sol(q, k, v, scale, beta, -1, 0, 0, return_stats,
                                     plan.protected_blocks, rows=plan.rows, keys=plan.keys,

@@ -145,7 +145,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == _native.ABI_VERSION == 10
+    assert native.sol_abi_version() == _native.ABI_VERSION == 11
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -164,9 +164,14 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     native = _native.library()
     strides = (ctypes.c_int64 * 3)(64 * 2 * 317, 128, 64)
     fake = ctypes.c_void_p(1 << 20)   # never dereferenced: validation fails first
-    rc = native.sol_dense_fwd(fake, strides, fake, strides, fake, strides, 1, 193, 317, 2, 64,
-                              float("nan"), fake, fake, None)
+    rc = native.sol_dense_fwd(fake, strides, None, 0, fake, strides, fake, strides, 1, 193, 317, 2, 64,
+                              float("nan"), fake, fake, None, None)
     assert rc == -1 and b"scale" in native.sol_last_error()
+    # A query or output index needs the sequence length it addresses.
+    for qi, oi in ((fake, None), (None, fake)):
+        rc = native.sol_dense_fwd(fake, strides, qi, 0, fake, strides, fake, strides, 1, 193, 317, 2, 64,
+                                  0.125, fake, fake, oi, None)
+        assert rc == -1 and b"sequence_length" in native.sol_last_error()
     attn = lambda index, n, form: native.sol_attention_fwd(  # noqa: E731
         fake, strides, index, n, 1, 193, 317, None, 2, 64, None, None, None, None, fake, fake, fake, fake,
         None, None, None, None, None, None, 0.125, 1.0, 1, 0, 0, fake, None, None, None, None, None, None, None, form, None)
@@ -257,6 +262,17 @@ def test_noalloc_rejects_problems_beyond_its_workspace_without_launching():
     rc = native.sol_attention_noalloc(fake, strides, fake, strides, fake, strides, 1, 200, 200, 16, 96,
                                       0.088, 1.0, 1, 0, 0, fake, None, None)
     assert rc == -1 and b"head_dim" in native.sol_last_error()
+    # Arguments the attention launch would reject are rejected before the
+    # pooling launch (nothing runs, no device is touched).
+    small = (ctypes.c_int64 * 3)(64 * 128 * 200, 64 * 128, 128)
+    for args, what in (((-0.1, 1.0, 1, 0, 0, fake), b"scale"),
+                       ((0.088, math.nan, 1, 0, 0, fake), b"beta"),
+                       ((0.088, 1.0, 1, -1, 0, fake), b"sink"),
+                       ((0.088, 1.0, 1, 0, 0, ctypes.c_void_p((1 << 20) + 2)), b"out")):
+        rc = native.sol_attention_noalloc(fake, small, fake, small, fake, small, 1, 200, 200, 64, 128,
+                                          *args, None, None)
+        msg = native.sol_last_error()
+        assert rc == -1 and msg.startswith(b"sol_attention_noalloc") and what in msg, msg
 
 
 def test_ragged_plan_matches_oracle_per_window():

@@ -98,3 +98,23 @@ def test_full_size_frame_windows(field):
     qrows = np.concatenate([np.arange(64 * b, 64 * b + 64) for b in sample])
     assert_close(full[rows[w][qrows].cuda()].cpu()[None], ref[:, qrows])
     np.testing.assert_array_equal(stats.exact_blocks[w:w + 1, sample].cpu().numpy(), counts[:, sample])
+
+
+def test_full_size_anchor_rows_over_every_key(field):
+    # Frame 0's queries attend all 84,672 keys (a window adapter's anchor rows,
+    # integrations/vdn.py:57-61): one dense launch gathering the rows and
+    # scattering the results; the oracle on three of its 63 query blocks.
+    q, k, v = (x[0] for x in field)
+    n = q.shape[0]
+    tpf = CFG["height"] * CFG["width"]
+    rows = torch.arange(tpf)[None]
+    plan = IndexedPlan.create(rows, torch.arange(n)[None], n).to("cuda")
+    assert plan.key_range == (0, n)
+    out = torch.zeros_like(q)
+    sol_attention_indexed(q, k, v, plan, beta=-math.inf, out=out)
+    assert bool((out[tpf:] == 0).all())
+    sample = [0, 31, 62]
+    qrows = np.concatenate([np.arange(64 * b, 64 * b + 64) for b in sample])
+    print(f"anchor rows: {tpf} queries x {n} keys, oracle on blocks {sample}", flush=True)
+    ref = orc.dense_oracle(q.cpu()[qrows][None], k.cpu()[None], v.cpu()[None])
+    assert_close(out[torch.as_tensor(qrows).cuda()].cpu()[None], ref)

@@ -66,7 +66,7 @@ def test_split_agrees_with_unsplit_and_forms_are_identical(case, monkeypatch):
     whole, whole_stats = sol_attention(q, k, v, **kw)
     assert torch.equal(split_stats.exact_blocks, whole_stats.exact_blocks)
     assert_close(split.cpu(), whole.cpu())
-    assert not torch.equal(split, whole)  # the split path ran
+    assert split_bytes(c, 1.0) > 0  # the split path ran (outputs may still agree bit for bit)
     monkeypatch.setattr(_native, "SPLIT_SINKS", True)
     forms = {}
     for g in (1, 2):

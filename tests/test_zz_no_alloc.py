@@ -5,6 +5,9 @@ in a row, the second smaller, so the shared device workspace is reused."""
 
 import ctypes
 import math
+import os
+import subprocess
+import sys
 
 import pytest
 import torch
@@ -55,3 +58,40 @@ def test_noalloc_matches_the_allocating_path_on_consecutive_calls():
         torch.cuda.synchronize()
         assert torch.equal(out, ref), f"case {i}"
         assert torch.equal(counts, ref_counts), f"case {i}"
+
+
+_FIRST_CALL = r"""
+import ctypes
+import torch
+from sol_attn_amd import _native
+from sol_testlib import block_smooth
+b, tq, tk, h, d = 1, 2048, 2048, 4, 128
+q = block_smooth(b, tq, h, d, seed=41, device="cuda")
+k = block_smooth(b, tk, h, d, seed=42, device="cuda")
+v = block_smooth(b, tk, h, d, seed=43, device="cuda")
+torch.cuda.synchronize()
+lib = _native.library()
+st = lambda x: (ctypes.c_int64 * 3)(*x.stride()[:3])
+out = torch.full_like(q, 7.0)
+rc = lib.sol_attention_noalloc(q.data_ptr(), st(q), k.data_ptr(), st(k), v.data_ptr(), st(v), b, tq, tk, h, d,
+                               d ** -0.5, 1.0, 1, 64, 128, out.data_ptr(), None,
+                               torch.cuda.current_stream().cuda_stream)
+assert rc == 0, lib.sol_last_error().decode()
+torch.cuda.synchronize()
+ref, _ = _native.launch_sol(q, k, v, d ** -0.5, 1.0, 1, 64, 128, False)
+assert torch.equal(out, ref)
+print("first-call noalloc ok", flush=True)
+"""
+
+
+def test_noalloc_as_the_first_call_of_a_process():
+    # The entry point is the process's first SOL launch: the device array is
+    # looked up and the kernels (split sink tiles included) loaded on it.
+    here = os.path.dirname(os.path.abspath(__file__))
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([here, os.path.join(here, "..", "solattn-amd_amd"),
+                                         env.get("PYTHONPATH", "")])
+    print("fresh process: noalloc first", flush=True)
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL], env=env, capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert "first-call noalloc ok" in res.stdout
