@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 11
+#define SOL_ABI_VERSION 12
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_TOKENS (1ll << 25) /* key_tokens of one pooling call (2^19 key blocks) */
 
@@ -145,8 +145,10 @@ int sol_key_covariance(const void* ctiles, const float* key_mean, const int32_t*
  * blocks (pair_strides is ignored).
  * A sink block selects every key block, so without the split its workgroup
  * ends long after the rest of a short launch.  The size is an upper bound
- * for every workgroup_form.  No counterpart in the reference (one Triton
- * program per query block). */
+ * for every workgroup_form.  Launches the small-launch kernel takes (see
+ * sol_attention_fwd's workgroup_form) split inside their workgroups and
+ * return 0.  No counterpart in the reference (one Triton program per query
+ * block). */
 int64_t sol_split_workspace_size(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
                                  int64_t head_dim, double beta, int64_t query_sink_tokens);
 
@@ -204,15 +206,36 @@ int64_t sol_route_workspace_size(int64_t batch, int64_t query_tokens, int64_t ke
  * matrix cores, Q8 = the query row at one scale s_q = max|q| / 127; routing,
  * centroid terms and P V stay BF16; sol_quantize_keys's rows_mode must be
  * nonzero exactly when tiles is NULL here.
- * workgroup_form: 0 picks the schedule by launch size (1 below 512 query-block
- * pairs, else 2); 1 or 2 force one or two query blocks per 4-wave workgroup
- * (bit-identical results).  No counterpart in the reference (one Triton
- * program per query block).
+ * workgroup_form: 0 picks the schedule by launch size: launches at finite
+ * or +INFINITY beta of at most 256 query blocks (over all entries and
+ * heads) whose keys span at most
+ * 64 (head_dim 64) or 32 (head_dim 128) blocks run one query block per
+ * workgroup with its key tiles split over 4 (2) groups of two waves, merged
+ * in LDS (outputs agree with the other forms to rounding; decisions and
+ * counts are the same); otherwise one query block per workgroup below 512
+ * query-block pairs, else 2.  1 or 2 force one or two query blocks per
+ * workgroup without the key split (bit-identical results).  No counterpart
+ * in the reference (one Triton program per query block).
+ * ctiles / key_mean / key_var: NULL at beta = -INFINITY (unused), or where
+ * sol_attention_pools_keys holds for the sizes and the call has plain K / V
+ * rows (tiles, key_lengths, query_index, key_cov, INT8 tiles and
+ * route_workspace NULL; workgroup_form 0): the attention launch then forms
+ * the block centroids and diagonal moments itself, bit for bit as
+ * sol_pool_kv does, and the whole call is one kernel launch.
  * Key blocks: with tiles NULL ("rows mode") the kernels DMA each key block's
  * rows straight from k / v (strides {batch, token, head} as in sol_pool_kv;
  * requires key_index-free, equal-length keys: key_lengths NULL, key_tokens >=
  * 64, token strides below 2^24 elements); otherwise from the tile pairs
  * sol_pool_kv wrote, and k / v are ignored (may be NULL). */
+/* 1 when sol_attention_fwd over plain K / V rows of these sizes pools the
+ * keys inside its one attention launch (ctiles, key_mean and key_var may be
+ * NULL): at least 64 and at most 1,024 keys (one pooling chunk of 16
+ * blocks) in a launch of the small-launch kernel (workgroup_form).  0
+ * otherwise.  No counterpart in the reference: it launches `_pool`,
+ * `_moments`, `_threshold` and `_sol` separately (kernels.py:203-225). */
+int sol_attention_pools_keys(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                             int64_t head_dim);
+
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t sequence_length, int64_t batch, int64_t query_tokens, int64_t key_tokens,
                       const int32_t* key_lengths, int64_t heads, int64_t head_dim,

@@ -18,7 +18,7 @@ import threading
 import torch
 
 BLOCK = 64
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -51,6 +51,7 @@ _SIGNATURES = {
     "sol_key_covariance_workspace_size": ([_i64, _i64, _i64], ctypes.c_int64),
     "sol_key_covariance": ([_p, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
     "sol_quantize_keys": ([_p, _i64p, _p, _p, _i64, _i64, _i64, _i64, _i64, _int, _p, _p, _p], ctypes.c_int),
+    "sol_attention_pools_keys": ([_i64, _i64, _i64, _i64, _i64], ctypes.c_int),
     "sol_attention_noalloc": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
                                _dbl, _dbl, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
 }
@@ -439,6 +440,24 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
     return out, counts, dbg
 
 
+# Short launches over at most 16 key blocks pool the keys inside the
+# attention launch (sol_attention_pools_keys): the whole call is one kernel.
+# False always runs the pooling kernel first.  Results are identical either
+# way (the same centroids and moments, bit for bit).
+SELF_POOLING = True
+
+
+def _self_pooled(k, v):
+    """The ``pool_kv`` record of keys the attention launch pools itself: plain
+    K / V rows and no pooled buffers."""
+    k, v = _rows(k), _rows(v)
+    b, nk, h, d = k.shape
+    return {"workspace": None, "shape": (b, h, d), "ctiles_ptr": None, "tiles_ptr": None,
+            "mean_ptr": None, "var_ptr": None, "cov_ptr": None, "key_tokens": nk,
+            "key_blocks": -(-nk // BLOCK), "key_lengths": None, "k8_ptr": None, "k8_scale_ptr": None,
+            "k": k, "v": v}
+
+
 def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=None,
                rows=None, keys=None, debug=False, key_lengths=None, out=None,
                threshold_estimator="diagonal_covariance", qk_precision="bf16"):
@@ -469,6 +488,14 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
             counts = torch.full((b, -(-nq // BLOCK), h), -(-k.shape[1] // BLOCK), device=q.device, dtype=torch.int32)
         return dense, counts
     stream = _stream(q.device)
+    if (SELF_POOLING and rows is None and keys is None and key_lengths is None and not debug
+            and qk_precision == "bf16" and threshold_estimator == "diagonal_covariance"
+            and WORKGROUP_FORM == 0 and ROUTE_PREPASS != "always" and rows_mode(k, v)
+            and library().sol_attention_pools_keys(q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3])):
+        # One launch: the attention kernel pools the keys itself.
+        out, counts, _ = attend(q, _self_pooled(k, v), scale, beta, local, kv_sink, q_sink, protection,
+                                out=out, stats=stats, stream=stream, strides=None)
+        return out, counts
     strides, pairing, means = _UNSET, None, None
     if PAIRING and OVERLAP_PAIRING:
         # Buffers come from the caller's stream and stay referenced until the

@@ -300,7 +300,8 @@ __device__ __forceinline__ void wait_ahead(int ahead) {
 // refill (TileRefill, Q8Refill) that DMAs tile ref into the LDS slot at lds.
 // R = 1: one slot, refilled after a barrier (latency
 // hidden by the other workgroups of the CU).  Two streams over the same ring
-// are separated by a barrier.
+// are separated by a barrier.  prologue() runs once the first tiles' DMA is
+// issued (or, for an empty stream, at once), before the first wait.
 // Selection predicate and the two tile consumers of a stream.
 template <typename Sel, typename Hit, typename Miss>
 struct TileRuns {
@@ -334,14 +335,23 @@ __device__ __forceinline__ auto kv_refills(const AttnParams& p, int b, int h, in
   }
 }
 
-template <int D, int NT, int R, typename Next, typename Make, typename Runs, typename Last>
+struct NoPrologue {
+  __device__ __forceinline__ void operator()() const {}
+};
+
+template <int D, int NT, int R, typename Next, typename Make, typename Runs, typename Last,
+          typename Prologue = NoPrologue>
 __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next, Make make,
-                                            Runs runs, Last last, int wave, int lane) {
+                                            Runs runs, Last last, int wave, int lane,
+                                            Prologue prologue = {}) {
   using S = Shape<D>;
   constexpr int kRounds = decltype(make(0, 0u))::kRounds;
   static_assert(R >= 1 && R <= 4 && (R & (R - 1)) == 0, "ring depth 1, 2 or 4");
   static_assert(R < 2 || (R - 2) * kRounds <= 63, "vmcnt range");
-  if (count <= 0) return;
+  if (count <= 0) {
+    prologue();
+    return;
+  }
   const uint32_t ring_lds = lds_address(ring);
   if constexpr (R == 1) {
     for (int i = 0; i < count; ++i) {
@@ -368,6 +378,9 @@ __device__ __forceinline__ void tile_stream(uint16_t* ring, int count, Next next
     ids[s] = s < count ? next() : 0;
     if (s < count) make(ids[s], ring_lds + uint32_t(s * S::TILE * 2)).all();
   }
+  // Work that overlaps the first tiles' DMA (LDS reads outside the ring slots
+  // the stream fills before its first barrier).
+  prologue();
   auto step = [&](int i, auto&& fn) {
     wait_ahead<kRounds>(min(R - 2, count - 1 - i));
     lds_barrier();
@@ -451,6 +464,72 @@ struct RangeCursor {
   int j;
   __device__ __forceinline__ int operator()() { return j++; }
 };
+
+// FP32 mean of a query block's qlen staged rows (LDS, row stride KS) at
+// feature f, in torch's cascade order: four sequential 16-row sums folded in
+// order (kernels.py:56).
+template <int D>
+__device__ __forceinline__ float query_mean(const uint16_t* rows, int qlen, int f) {
+  float tot = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    // The chunk's 16 values are read first (every staged row exists), so the
+    // reads overlap; the sum then takes the block's rows in order.
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = bf16_bits_to_f32(rows[(16 * c + i) * Shape<D>::KS + f]);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (16 * c + i < qlen) sum = __fadd_rn(sum, x[i]);
+    tot = __fadd_rn(tot, sum);
+  }
+  return __fdiv_rn(tot, float(qlen));
+}
+
+// The cutoff from the workgroup-summed terms: sum Qc mu + beta sqrt(the
+// quadratic form), which the full covariance may round below 0
+// (kernels.py:58-63).
+__device__ __forceinline__ float cutoff_value(const AttnParams& p, float lin0, float lin1, float quad0,
+                                              float quad1) {
+  const float quad = quad0 + quad1;
+  return (lin0 + lin1) + p.beta * sqrtf(p.cov ? fmaxf(quad, 0.f) : quad);
+}
+
+// Routing decision for key block j (row r of the centroid tile in LDS at
+// buf) of query block qb in entry b: the proxy Qc . Kc_j over this lane's
+// feature half (qm: the block's FP32 query mean), summed across the lane
+// pair, above the cutoff -- or a key sink, local or plan-protected block
+// (kernels.py:129-143).  Writes the diagnostics of row dbg_row.
+template <int D>
+__device__ __forceinline__ bool route_block(const AttnParams& p, const uint16_t* buf, const float* qm, float cut,
+                                            int r, int j, int b, int qb, int hh, int64_t dbg_row) {
+  using S = Shape<D>;
+  using TL = TileLayout<D>;
+  bool sel = false;
+  if (p.force == 0) {
+    const int c0 = fresh(hh) * (S::DC / 2);  // first 16-byte chunk of this lane's feature half
+    float part[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < S::DC / 2; ++c) {
+      const int cc = c0 + c;
+      const u32x4 x = *reinterpret_cast<const u32x4*>(buf + TL::k_offset(r, cc));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t w = x[e >> 1];
+        part[e & 3] = fmaf(qm[8 * cc + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)), part[e & 3]);
+      }
+    }
+    const float proxy = pair_sum((part[0] + part[1]) + (part[2] + part[3]));
+    sel = proxy > cut;
+    if (p.dbg_proxy && hh == 0) p.dbg_proxy[dbg_row + j] = proxy * p.scale;
+  }
+  sel = sel || (p.local_blocks >= 0 && abs(j - qb) <= p.local_blocks) || j < p.kv_sink_blocks ||
+        qb < p.q_sink_blocks;
+  if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * p.NKB + j] != 0;
+  if (p.dbg_selected && hh == 0) p.dbg_selected[dbg_row + j] = sel ? 1 : 0;
+  return sel;
+}
 
 }  // namespace
 
@@ -562,18 +641,7 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   const bool routed = p.mask != nullptr;  // decisions precomputed by route_kernel
   if (p.force == 0 && !routed) {
     const int qlen = live ? min(kBlock, p.Tq - qb * kBlock) : 1;
-    if (lt < D) {
-      float tot = 0.f;
-      for (int c = 0; c < 4; ++c) {
-        float sum = 0.f;
-        for (int i = 0; i < 16; ++i) {
-          const int r = 16 * c + i;
-          if (r < qlen) sum = __fadd_rn(sum, bf16_bits_to_f32(ring[(qg * kBlock + r) * S::KS + lt]));
-        }
-        tot = __fadd_rn(tot, sum);
-      }
-      s_qm[qg][lt] = __fdiv_rn(tot, float(qlen));
-    }
+    if (lt < D) s_qm[qg][lt] = query_mean<D>(ring + qg * kBlock * S::KS, qlen, lt);
     __syncthreads();
     float a = 0.f, g = 0.f;
     if (lt < D) {
@@ -599,10 +667,7 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
       s_red[qg][2 + qh] = g;
     }
     __syncthreads();
-    if (tid < G) {
-      const float quad = s_red[tid][2] + s_red[tid][3];  // the full quadratic form may round below 0
-      s_cut[tid] = (s_red[tid][0] + s_red[tid][1]) + p.beta * sqrtf(p.cov ? fmaxf(quad, 0.f) : quad);
-    }
+    if (tid < G) s_cut[tid] = cutoff_value(p, s_red[tid][0], s_red[tid][1], s_red[tid][2], s_red[tid][3]);
   }
   __syncthreads();  // cutoffs published; Q staging is dead and the ring is free
   const int64_t dbg_row = ((int64_t(b) * p.NQB + qb) * p.H + h) * p.NKB;
@@ -677,30 +742,8 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
           const int r = fresh(32 * qh + col);  // centroid row inside the tile
           const int j = kBlock * ct + r;
           bool sel = false;
-          if (live && j >= seg + r0 && j < seg + r1) {
-            if (p.force == 0) {
-              const int c0 = fresh(hh) * (S::DC / 2);  // first 16-byte chunk of this lane's feature half
-              float part[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int c = 0; c < S::DC / 2; ++c) {
-                const int cc = c0 + c;
-                const u32x4 x = *reinterpret_cast<const u32x4*>(buf + TL::k_offset(r, cc));
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                  const uint32_t w = x[e >> 1];
-                  part[e & 3] = fmaf(s_qm[qg][8 * cc + e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)),
-                                     part[e & 3]);
-                }
-              }
-              const float proxy = pair_sum((part[0] + part[1]) + (part[2] + part[3]));
-              sel = proxy > s_cut[qg];
-              if (p.dbg_proxy && hh == 0) p.dbg_proxy[dbg_row + j] = proxy * p.scale;
-            }
-            sel = sel || (p.local_blocks >= 0 && abs(j - qb) <= p.local_blocks) || j < p.kv_sink_blocks ||
-                  qb < p.q_sink_blocks;
-            if (p.protection) sel = sel || p.protection[(int64_t(b) * p.NQB + qb) * p.NKB + j] != 0;
-            if (p.dbg_selected && hh == 0) p.dbg_selected[dbg_row + j] = sel ? 1 : 0;
-          }
+          if (live && j >= seg + r0 && j < seg + r1)
+            sel = route_block<D>(p, buf, s_qm[qg], s_cut[qg], r, j, b, qb, hh, dbg_row);
           const uint64_t bal = __ballot(sel);
           if (lane == 0) s_mask[qg][2 * (ct - ct0) + qh] = uint32_t(bal);
           lds_barrier();  // publishes the mask words
@@ -804,6 +847,394 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
 
   // 5. Normalise and store.
   if (live) store_output<D>(p, b, h, qb * kBlock + myq, hh, st);
+}
+
+// The exact tiles of key-split group `grp` of KS: positions grp, grp + KS,
+// ... of the query block's selected blocks (UnionCursor<1> tags), one per
+// stream step for every group; a group whose list ends first gets the
+// cursor's (valid, unselected) padding tags for the remaining step.
+template <int KS>
+struct SplitCursor {
+  UnionCursor<1> all;
+  int grp;
+  __device__ __forceinline__ int operator()() {
+    int tag = 0;
+#pragma unroll
+    for (int g = 0; g < KS; ++g) {
+      const int t = all();
+      if (g == grp) tag = t;
+    }
+    return tag;
+  }
+};
+
+// Small launches (one query block per workgroup, a few hundred workgroups at
+// most): the queries' dependency chains, not the matrix cores, set the time
+// -- a two-wave workgroup per query block leaves three of a CU's four SIMDs
+// idle and exposes every load, barrier and accumulation latency of its tile
+// chain (a query-sink block's chain is every key block).  Here KS groups of
+// two waves share a query block: wave (grp, qh) owns queries 32 qh .. +31 of
+// it, and group grp attends exact tiles grp, grp + KS, ... of its selected
+// blocks through a two-slot ring of its own, every group stepping in the
+// same workgroup barrier, so a chain of n tiles takes ceil(n / KS) steps.
+// Group 0 routes and adds the centroid contributions (skipped for a tile
+// with no approximated block); at the end every group publishes its
+// online-softmax state in LDS and merges and stores a share of the output
+// features (m = max m_g, acc and den weighted by 2^(m_g - m), groups in
+// order).  Decisions, counts and diagnostics are the
+// one-block kernel's; the output agrees with it to rounding (other partial
+// sums).  POOL (plain K / V rows, at most one pooling chunk of key blocks,
+// no centroid tiles given): every workgroup forms its head's block centroids
+// and diagonal moments in LDS in the pooling kernel's order and arithmetic
+// (bit-identical values), so the whole call is this one launch.  Finite and
+// +inf beta only (beta = -inf launches take sol_attention_kernel).
+// The ring takes ~130 KB of LDS: one workgroup per CU, KS / 2 waves per SIMD.
+template <int D, int KS, bool KT, bool POOL>
+__global__ __launch_bounds__(128 * KS, KS / 2) void sol_small_kernel(AttnParams p) {
+  using S = Shape<D>;
+  using TL = TileLayout<D>;
+  constexpr int NT = 128 * KS;
+  constexpr int kMaskWords = kMaxKeyBlocks / 32;
+  constexpr int NC = S::DT * 4;            // 4-feature output chunks per lane
+  constexpr int kStateFloats = 4 * NC + 2;  // per lane: acc, m, den
+  constexpr int QPT = kBlock * S::DC / NT;  // Q staging chunks per thread
+  static_assert(!POOL || !KT, "in-kernel pooling reads plain K / V rows");
+  static_assert(QPT * NT == kBlock * S::DC, "Q rows split evenly over the workgroup");
+  static_assert(KS * 2 * kWave * kStateFloats * 4 <= 2 * KS * S::TILE * 2, "merge records fit the ring");
+  // Group g's ring slots at 2 g TILE (the centroid pass streams through the
+  // first two); Q staging and the pooled centroid tile alias them early on.
+  __shared__ __align__(256) uint16_t ring[2 * KS * S::TILE];
+  __shared__ float s_qm[D];
+  __shared__ float s_red[4];
+  __shared__ float s_mom[2][POOL ? D : 1];  // pooled key mean, variance
+  __shared__ uint32_t s_mask[kMaskWords];
+
+  const int nbh = p.B * p.H;
+  const int bh = blockIdx.x % nbh, qb = blockIdx.x / nbh;  // every head's first blocks dispatch first
+  const int h = bh % p.H, b = bh / p.H;
+  const int64_t head = int64_t(b) * p.H + h;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 1, qh = wave & 1;
+  const int col = lane & 31, hh = lane >> 5;
+  const int myq = 32 * qh + col;
+  const int tk = batch_tokens(p.klen, b, p.Tk);
+  const int nkb = (tk + kBlock - 1) / kBlock;
+  const int qlen = min(kBlock, p.Tq - qb * kBlock);
+  const float scale_log2 = p.scale_log2;
+  const bool routed = p.mask != nullptr;
+  uint16_t* const ctile = ring + S::TILE;  // the pooled centroid tile (slot 1)
+
+  // 1. Q rows -> LDS (slot 0) -> fragments; with POOL, the head's centroids
+  // -> slot 1 in the tile layout (rows past the last block zero).  Every
+  // global load is issued before the first LDS store that waits on one.
+  u32x4 qx[QPT];
+#pragma unroll
+  for (int i = 0; i < QPT; ++i) {
+    const int idx = tid + i * NT, r = idx / S::DC, c = idx % S::DC;
+    const int t = qb * kBlock + r;
+    qx[i] = t < p.Tq ? load16(p.q.row(b, t, h) + 8 * c) : zero_u32x4();
+  }
+  auto stage_q = [&] {
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int idx = tid + i * NT, r = idx / S::DC, c = idx % S::DC;
+      *reinterpret_cast<u32x4*>(ring + r * S::KS + 8 * c) = qx[i];
+    }
+  };
+  // Pooling units: block jb of K (u < 16) or of V (u - 16), 16 rows x 16
+  // bytes per lane, summed as the pooling kernel sums them.
+  constexpr int DC = D / 8;
+  constexpr int LPB = DC * 4;       // lanes per key block: 4 row quarters x DC chunks
+  constexpr int BPI = kWave / LPB;  // blocks per wave and pass
+  constexpr int PER_PASS = 2 * KS * BPI;
+  constexpr int NU = 2 * kPoolChunk / PER_PASS;  // units per lane
+  // One K and one V unit per lane: V's centroids are finished while the
+  // workgroup routes, so its loads stay in flight through the cutoff.
+  constexpr bool kLateV = POOL && NU == 2;
+  static_assert(!POOL || NU % 2 == 0, "K and V blocks split evenly over the passes");
+  const int sub = lane / LPB, r4 = (lane % LPB) / DC, dc = lane % DC;
+  auto load_unit = [&](int u, u32x4 (&x)[16]) {
+    const int jb = u % kPoolChunk;
+    const int len = jb < nkb ? min(kBlock, tk - kBlock * jb) : 0;
+    if (len > 0)
+      load_rows16<16>(u >= kPoolChunk ? p.v : p.k, b, kBlock * jb + 16 * r4, kBlock * jb + len - 1, h, 8 * dc, x);
+    return len;
+  };
+  auto finish_unit = [&](int u, const u32x4 (&x)[16], int len) {
+    float sm[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm[e] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (16 * r4 + i < len) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t w = x[i][e >> 1];
+          sm[e] = __fadd_rn(sm[e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)));
+        }
+      }
+    }
+    float t1[8], t2[8], t3[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      t1[e] = __shfl(sm[e], lane + DC);
+      t2[e] = __shfl(sm[e], lane + 2 * DC);
+      t3[e] = __shfl(sm[e], lane + 3 * DC);
+    }
+    if (r4 == 0) {
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        float m0 = 0.f, m1 = 0.f;
+        if (len > 0) {
+          m0 = __fdiv_rn(__fadd_rn(__fadd_rn(__fadd_rn(sm[e], t1[e]), t2[e]), t3[e]), float(len));
+          m1 = __fdiv_rn(__fadd_rn(__fadd_rn(__fadd_rn(sm[e + 1], t1[e + 1]), t2[e + 1]), t3[e + 1]), float(len));
+        }
+        o[e >> 1] = pack_bf16x2(m0, m1);
+      }
+      const int jb = u % kPoolChunk;
+      *reinterpret_cast<u32x4*>(ctile + (u >= kPoolChunk ? TL::kElems + TL::v_offset(jb, dc) : TL::k_offset(jb, dc))) = o;
+    }
+  };
+  const int u_first = wave * BPI + sub;
+  u32x4 xv[kLateV ? 16 : 1];
+  int len_v = 0;
+  if constexpr (POOL) {
+    if constexpr (kLateV) {
+      u32x4 xk[16];
+      const int len_k = load_unit(u_first, xk);
+      len_v = load_unit(u_first + PER_PASS, xv);
+      stage_q();
+      finish_unit(u_first, xk, len_k);
+    } else {
+      // Two units per lane in flight at once.
+#pragma unroll 1
+      for (int u0 = 0; u0 < 2 * kPoolChunk; u0 += 2 * PER_PASS) {
+        const int ua = u0 + u_first, ub = ua + PER_PASS;
+        u32x4 xa[16], xb[16];
+        const int la = load_unit(ua, xa);
+        const int lb = load_unit(ub, xb);
+        if (u0 == 0) stage_q();
+        finish_unit(ua, xa, la);
+        finish_unit(ub, xb, lb);
+      }
+    }
+    // Rows kPoolChunk .. 63 of both tiles are zero.
+    for (int idx = tid; idx < 2 * (kBlock - kPoolChunk) * DC; idx += NT) {
+      const int kv = idx / ((kBlock - kPoolChunk) * DC), rest = idx % ((kBlock - kPoolChunk) * DC);
+      const int r = kPoolChunk + rest / DC, c = rest % DC;
+      *reinterpret_cast<u32x4*>(ctile + (kv ? TL::kElems + TL::v_offset(r, c) : TL::k_offset(r, c))) = zero_u32x4();
+    }
+  } else {
+    stage_q();
+  }
+  __syncthreads();
+  bf16x8 qf[S::KT];
+  {
+    const uint16_t* qrow = ring + myq * S::KS;
+#pragma unroll
+    for (int ks = 0; ks < S::KT; ++ks)
+      qf[ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(qrow + ks * 16 + 8 * hh));
+  }
+  if constexpr (POOL) {
+    // Diagonal moments of the BF16 centroids: sequential sums over the
+    // blocks, E[x^2] - mu^2 clamped at 0, each step rounded on its own.
+    if (tid < D) {
+      float s1 = 0.f, s2 = 0.f;
+      for (int jb = 0; jb < nkb; ++jb) {
+        const float x = bf16_bits_to_f32(ctile[TL::k_offset(jb, tid / 8) + tid % 8]);
+        s1 = __fadd_rn(s1, x);
+        s2 = __fadd_rn(s2, __fmul_rn(x, x));
+      }
+      const float n = float(nkb);
+      const float m = __fdiv_rn(s1, n);
+      const float v = __fsub_rn(__fdiv_rn(s2, n), __fmul_rn(m, m));
+      s_mom[0][tid] = m;
+      s_mom[1][tid] = v > 0.f ? v : 0.f;
+    }
+  }
+
+  // 2. In-kernel routing: query mean and cutoff (group 0's threads sum; every
+  // thread forms the cutoff from the published sums).
+  float cut = 0.f;
+  if (p.force == 0 && !routed) {
+    if (tid < D) s_qm[tid] = query_mean<D>(ring, qlen, tid);
+    __syncthreads();  // also: every read of the Q staging rows is done
+    float a = 0.f, g = 0.f;
+    if (tid < D) {
+      const float qm = s_qm[tid];
+      const float mu = POOL ? s_mom[0][tid] : p.mean[head * D + tid];
+      a = qm * mu;
+      if (p.cov) {
+        const float* row = p.cov + (head * D + tid) * D;
+        float sq = 0.f;
+        for (int e = 0; e < D; ++e) sq = fmaf(row[e], s_qm[e], sq);
+        g = qm * sq;
+      } else {
+        g = qm * qm * (POOL ? s_mom[1][tid] : p.var[head * D + tid]);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      a += __shfl_xor(a, off);
+      g += __shfl_xor(g, off);
+    }
+    if (wave < 2 && lane == 0) {
+      s_red[wave] = a;
+      s_red[2 + wave] = g;
+    }
+    __syncthreads();
+    cut = cutoff_value(p, s_red[0], s_red[1], s_red[2], s_red[3]);
+  } else {
+    __syncthreads();  // every wave's Q fragments are read: the ring is free
+  }
+  const int64_t dbg_row = ((int64_t(b) * p.NQB + qb) * p.H + h) * p.NKB;
+  if (p.dbg_cutoff && tid == 0 && !routed)
+    p.dbg_cutoff[(int64_t(b) * p.NQB + qb) * p.H + h] = p.force == 0 ? cut * p.scale : -kNegInf;
+
+  State<D> st;
+  state_init(st);
+  const int nwords = (nkb + 31) / 32;
+  {
+    // 3. Centroid pass (group 0 attends; every wave takes part in the
+    // barriers and the ring's DMA).  Launches at beta = -inf take
+    // sol_attention_kernel.
+    if (routed) {
+      for (int w = tid; w < nwords; w += NT) s_mask[w] = p.mask[(head * p.NQB + qb) * p.NW + w];
+      __syncthreads();
+    }
+    if constexpr (POOL) {
+      // The one centroid tile sits in slot 1: route from it now (and finish
+      // its V rows); its contributions run in the exact stream's prologue,
+      // over the first exact tiles' DMA (group 0's first slot is slot 0).
+      if (!routed && grp == 0) {
+        const int j = fresh(myq);
+        const bool sel = j < nkb && route_block<D>(p, ctile, s_qm, cut, j, j, b, qb, hh, dbg_row);
+        const uint64_t bal = __ballot(sel);
+        if (lane == 0) s_mask[qh] = uint32_t(bal);
+      }
+      if constexpr (kLateV) finish_unit(u_first + PER_PASS, xv, len_v);
+      lds_barrier();  // publishes the mask words and the V centroids
+    } else {
+      auto process = [&](const uint16_t* buf, int ct, const auto& refill) {
+        if (!routed) {
+          if (grp == 0) {
+            const int r = fresh(myq);  // centroid row inside the tile
+            const int j = kBlock * ct + r;
+            const bool sel = j < nkb && route_block<D>(p, buf, s_qm, cut, r, j, b, qb, hh, dbg_row);
+            const uint64_t bal = __ballot(sel);
+            if (lane == 0) s_mask[2 * ct + qh] = uint32_t(bal);
+          }
+          lds_barrier();  // publishes the mask words
+        }
+        // The workgroup's one query block decides for every wave: a tile
+        // without approximated blocks (a query-sink block's) is skipped.
+        const uint64_t approx = tile_approx(s_mask, ct, 0, nkb);
+        if (grp == 0 && approx != 0ull) {
+          centroid_tile<D>(st, buf, ct, approx, tk, qf, col, hh, scale_log2, refill);
+        } else {
+          refill.all();
+        }
+      };
+      const uint16_t* ctiles = p.ctiles + head * p.NCT * S::TILE;
+      auto always = [](int) { return true; };
+      const auto crefill = bf16_refills<D, NT>([=](int ct) { return ctiles + int64_t(ct) * S::TILE; }, wave, lane);
+      tile_stream<D, NT, 2>(ring, (nkb + kBlock - 1) / kBlock, RangeCursor{0}, crefill,
+                            tile_runs(always, process, process), process, wave, lane);
+      lds_barrier();  // the ring's centroid tiles and the masks are settled
+    }
+  }
+  int nsel = 0;
+  if (p.counts && tid == 0)
+    for (int w = 0; w < nwords; ++w) nsel += __builtin_popcount(s_mask[w] & uint32_t(bit_range64(0, nkb - 32 * w)));
+
+  // 4. Exact pass: group grp's share of the selected blocks, ascending.
+  {
+    UnionCursor<1> all{s_mask, s_mask, kMaskWords, 0, nkb, 0};
+    const int steps = (all.count() + KS - 1) / KS;
+    const int wg = wave & 1;  // the wave inside its group
+    const auto kv = kv_refills<D, 128, KT>(p, b, h, wg, lane);
+    auto selected = [](int tag) { return (tag & 1) != 0; };
+    auto hit = [&](const uint16_t* buf, int, const auto& refill) {
+      full_tile<D>(st, buf, qf, col, hh, scale_log2, refill);
+    };
+    auto miss = [&](const uint16_t*, int, const auto& refill) { refill.all(); };
+    tile_stream<D, 128, 2>(
+        ring + grp * 2 * S::TILE, steps, SplitCursor<KS>{all, grp},
+        [=](int tag, uint32_t lds) { return kv(tag >> 1, lds); }, tile_runs(selected, hit, miss),
+        [&](const uint16_t* buf, int tag, const auto& refill) {
+          if (tag & 1) {
+            exact_tile<D, !KT>(st, buf, tag >> 1, tk, qf, col, hh, scale_log2, refill);
+          } else {
+            refill.all();
+          }
+        },
+        wg, lane, [&] {
+          if constexpr (POOL) {
+            const uint64_t approx = tile_approx(s_mask, 0, 0, nkb);
+            if (grp == 0 && approx != 0ull)
+              centroid_tile<D>(st, ctile, 0, approx, tk, qf, col, hh, scale_log2, NoRefill{});
+          }
+        });
+  }
+
+  // 5. Merge and store, spread over the groups: every group publishes its
+  // state; group g then combines output chunks c = g, g + KS, ... of every
+  // state -- O = sum_s 2^(m_s - m) acc_s / sum_s 2^(m_s - m) den_s, m =
+  // max_s m_s, states in order -- and stores them (store_output's rows).
+  __syncthreads();  // every group's stream is done with the ring
+  float* rec = reinterpret_cast<float*>(ring);
+  auto state = [&](int g) { return rec + (g * 2 + qh) * (kWave * kStateFloats); };
+  {
+    float* mine = state(grp);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      f32x4 x;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = st.acc[c / 4][4 * (c % 4) + i];
+      *reinterpret_cast<f32x4*>(mine + (c * kWave + lane) * 4) = x;
+    }
+    mine[4 * NC * kWave + lane] = st.m;
+    mine[4 * NC * kWave + kWave + lane] = st.den;
+  }
+  __syncthreads();
+  float ms[KS], m = kNegInf;
+#pragma unroll
+  for (int g = 0; g < KS; ++g) {
+    ms[g] = state(g)[4 * NC * kWave + lane];
+    m = fmaxf(m, ms[g]);
+  }
+  float w[KS], den = 0.f;
+#pragma unroll
+  for (int g = 0; g < KS; ++g) {
+    w[g] = ms[g] == kNegInf ? 0.f : fast_exp2(ms[g] - m);
+    den = den + w[g] * state(g)[4 * NC * kWave + kWave + lane];
+  }
+  den = pair_sum(den);
+  if (p.counts && tid == 0) p.counts[(int64_t(b) * p.NQB + qb) * p.H + h] = nsel;
+  const int t = qb * kBlock + myq;
+  if (t >= p.Tq) return;
+  int64_t row = int64_t(b) * p.Tq + t;
+  if (p.out_index) {
+    row = p.out_index[row];
+    if (row < 0 || row >= p.out_rows) return;  // outside the output: not stored
+  }
+  uint16_t* orow = p.out + (row * p.H + h) * D;
+#pragma unroll
+  for (int c = grp; c < NC; c += KS) {
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < KS; ++g) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(state(g) + (c * kWave + lane) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = o[i] + w[g] * x[i];
+    }
+    u32x2 v;
+    v[0] = pack_bf16x2(__fdiv_rn(o[0], den), __fdiv_rn(o[1], den));
+    v[1] = pack_bf16x2(__fdiv_rn(o[2], den), __fdiv_rn(o[3], den));
+    *reinterpret_cast<u32x2*>(orow + (c / 4) * 32 + 8 * (c % 4) + 4 * hh) = v;
+  }
 }
 
 template <int D, bool KT>
@@ -966,6 +1397,17 @@ void launch_sol_group(const AttnParams& p, hipStream_t stream) {
   }
 }
 
+template <int D, int KS>
+void launch_small(const AttnParams& p, hipStream_t stream) {
+  const dim3 grid(unsigned(p.B * p.H * p.NQB)), block(128 * KS);
+  if (p.tiles)
+    hipLaunchKernelGGL((sol_small_kernel<D, KS, true, false>), grid, block, 0, stream, p);
+  else if (!p.ctiles)
+    hipLaunchKernelGGL((sol_small_kernel<D, KS, false, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((sol_small_kernel<D, KS, false, false>), grid, block, 0, stream, p);
+}
+
 hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
   // Routing first when its masks go to the routing workspace (beta = -inf
   // selects every block and needs none; without a workspace the attention
@@ -973,6 +1415,19 @@ hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
   if (p.force != 1 && p.mask) {
     const hipError_t err = launch_route(p, D, stream);
     if (err != hipSuccess) return err;
+  }
+  // Small launches: one query block per workgroup, key-split groups (the
+  // caller passes no split workspace for them).  A forced workgroup form and
+  // beta = -inf keep sol_attention_kernel, whose every-block-exact path
+  // equals the dense kernel bit for bit.
+  const int ks = p.workgroup_form == 0 && !p.k8 && p.splits == 1 && p.force != 1
+                     ? small_key_split(int64_t(p.B) * p.H * p.NQB, p.NKB, D) : 0;
+  if (ks) {
+    if (D == 128)
+      launch_small<128, 2>(p, stream);
+    else
+      launch_small<64, 4>(p, stream);
+    return hipGetLastError();
   }
   int g = int64_t(p.B) * p.H * ((p.NQB + 1) / 2) < kSmallLaunchGroups ? 1 : 2;
   if (p.workgroup_form == 1 || p.workgroup_form == 2) g = p.workgroup_form;

@@ -115,12 +115,23 @@ int64_t split_bytes(int64_t bh, int64_t q_sink_blocks, int64_t splits, int64_t h
 
 int sink_splits(int64_t bh, int64_t nqb, int64_t nkb, int64_t q_sink_blocks, int force, int64_t head_dim) {
   const bool one_block_groups = bh * ((nqb + 1) / 2) < 512;
+  // Launches of the small kernel split every query block's chain inside its
+  // workgroup instead.
+  if (sol::small_key_split(bh * nqb, nkb, head_dim)) return 1;
   if (force == 1 || q_sink_blocks < 2 || 4 * q_sink_blocks > nqb || nkb > sol::kMaxKeyBlocks ||
       !(one_block_groups || (force == 2 && bh * nqb <= 8192)))
     return 1;
   int64_t s = std::min<int64_t>(8, nkb / 16);
   while (s > 1 && split_bytes(bh, q_sink_blocks, s, head_dim) > kSplitBytesMax) --s;
   return int(std::max<int64_t>(s, 1));
+}
+
+// Whether a launch of these sizes over plain K / V rows runs as one kernel
+// that pools the keys itself (sol_attention_pools_keys).
+bool pools_keys(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads, int64_t head_dim) {
+  const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
+  return key_tokens >= SOL_BLOCK && nkb <= sol::kPoolChunk &&
+         sol::small_key_split(batch * heads * cdiv(query_tokens, SOL_BLOCK), nkb, head_dim) > 0;
 }
 
 int64_t sink_blocks(int64_t query_sink_tokens) {
@@ -365,6 +376,13 @@ int64_t sol_route_workspace_size(int64_t batch, int64_t query_tokens, int64_t ke
   return route_mask_bytes(batch, query_tokens, key_tokens, heads);
 }
 
+int sol_attention_pools_keys(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                             int64_t head_dim) {
+  return shape_ok(batch, query_tokens, heads, head_dim) && key_tokens > 0 && key_tokens < (int64_t(1) << 30) &&
+                 pools_keys(batch, query_tokens, key_tokens, heads, head_dim)
+             ? 1 : 0;
+}
+
 int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* query_index,
                       int64_t sequence_length, int64_t batch, int64_t query_tokens,
                       int64_t key_tokens,
@@ -392,7 +410,16 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
   if ((qk_int8_tiles == nullptr) != (qk_int8_scales == nullptr) || (qk_int8_tiles && !aligned16(qk_int8_tiles)))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: qk_int8_tiles (16-byte aligned) and qk_int8_scales go together");
   const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
-  if (!ctiles || !aligned16(ctiles) || (tiles && !aligned16(tiles)) ||
+  // Without centroid tiles the launch pools the keys itself (or, at beta =
+  // -inf, needs none).
+  const bool self_pooled = !ctiles && force != 1;
+  if (self_pooled && (tiles || key_lengths || query_index || key_cov || qk_int8_tiles || route_workspace ||
+                      workgroup_form != 0 || !pools_keys(batch, query_tokens, key_tokens, heads, head_dim)))
+    return fail(SOL_ERR_INVALID,
+                "sol_attention_fwd: ctiles may be NULL only at beta = -inf or where sol_attention_pools_keys "
+                "holds (plain K / V rows, no key_lengths, query_index, key_cov, INT8 tiles or route_workspace, "
+                "workgroup_form 0)");
+  if ((ctiles && !aligned16(ctiles)) || (tiles && !aligned16(tiles)) ||
       (split_workspace && !aligned16(split_workspace)) || (route_workspace && !aligned16(route_workspace)))
     return fail(SOL_ERR_INVALID,
                 "sol_attention_fwd: tiles/ctiles/split_workspace/route_workspace must be 16-byte aligned "
@@ -403,7 +430,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
     const int rc = rows_mode_ok("sol_attention_fwd", k, k_strides, v, v_strides, key_lengths, key_tokens);
     if (rc != SOL_OK) return rc;
   }
-  if (force == 0 && (!key_mean || !key_var))
+  if (force == 0 && !self_pooled && (!key_mean || !key_var))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
   const int64_t nqb = cdiv(query_tokens, SOL_BLOCK);
@@ -548,13 +575,20 @@ int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k
   const int arc = attention_args_ok("sol_attention_noalloc", q, q_strides, false, batch, query_tokens, heads,
                                     scale, beta, kv_sink_tokens, query_sink_tokens, out);
   if (arc != SOL_OK) return arc;
+  const bool rows = rows_mode_possible(nullptr, nullptr, key_tokens, k_strides, v_strides);
+  // One attention launch that pools the keys itself: no workspace at all.
+  if (rows && !(std::isinf(beta) && beta < 0) && pools_keys(batch, query_tokens, key_tokens, heads, head_dim))
+    return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads, head_dim,
+                             k, k_strides, v, v_strides, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                             nullptr, nullptr, nullptr, nullptr, scale, beta, local_blocks, kv_sink_tokens,
+                             query_sink_tokens, out, nullptr, counts, nullptr, nullptr, nullptr, nullptr, nullptr,
+                             0, stream);
   // The sol_pool_kv buffers, 256-byte aligned, in the order sol_pool_sizes lists them.
   int64_t sizes[4];
   if (sol_pool_sizes(batch, key_tokens, heads, head_dim, sizes) != SOL_OK) return SOL_ERR_INVALID;
   const bool moments = std::isfinite(beta);
   // Rows mode needs no block tiles; fewer than 64 keys (or huge token
   // strides) take them in the workspace.
-  const bool rows = rows_mode_possible(nullptr, nullptr, key_tokens, k_strides, v_strides);
   const int64_t off_tiles = align256(sizes[0]);
   const int64_t off_sums = off_tiles + (rows ? 0 : align256(sizes[1]));
   const int64_t off_mean = off_sums + align256(sizes[2]);

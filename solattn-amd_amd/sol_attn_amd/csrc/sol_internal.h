@@ -110,6 +110,21 @@ struct QuantParams {
   int shifted;          // partial last blocks as the rows-mode attention tiles hold them
 };
 
+// Key-split groups of sol_small_kernel for a launch of `blocks` query blocks
+// (over all entries and heads) against nkb key blocks, or 0 when the launch
+// takes sol_attention_kernel.  Small launches (at most kSmallBlocks query
+// blocks, a workgroup each) leave most SIMDs idle, so their time is one
+// workgroup's tile chain: KS groups of two waves split it KS ways, within the
+// LDS of two ring slots per group (4 groups at D = 64, 2 at D = 128), while
+// the chain stays at most kSmallChain steps.  Longer key sequences go to the
+// one-block kernel, whose query-sink tiles split over workgroups instead.
+constexpr int64_t kSmallBlocks = 256;
+constexpr int64_t kSmallChain = 16;
+inline int small_key_split(int64_t blocks, int64_t nkb, int64_t head_dim) {
+  const int ks = head_dim == 64 ? 4 : 2;
+  return blocks <= kSmallBlocks && nkb <= kSmallChain * ks ? ks : 0;
+}
+
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream);
 hipError_t launch_quantize_keys(const QuantParams& p, int D, hipStream_t stream);
 hipError_t launch_route(const AttnParams& p, int D, hipStream_t stream);

@@ -5,8 +5,8 @@ rows and scatters the results inside the kernel (``sol_dense_fwd`` with
 ``query_index`` / ``out_index``).  ``sol_attention_indexed`` takes it at
 beta = -inf when every window's keys are one and the same contiguous range.
 
-Checked against the dense oracle on the gathered rows; against the SOL
-kernel's beta = -inf path on the same plan, which reads zero-padded block
+Checked against the dense oracle on the gathered rows; against the one-block
+SOL kernel's beta = -inf path on the same plan, which reads zero-padded block
 tiles: bit-identical when the keys fill whole 64-key blocks, equal to
 rounding otherwise (rows mode reads a partial last block as the range's last
 64 rows, so its valid keys meet the matrix cores' sums in other groups); and
@@ -21,7 +21,7 @@ import pytest
 import torch
 
 from oracle import sol_oracle as orc
-from sol_attn_amd import IndexedPlan, sol_attention_indexed
+from sol_attn_amd import IndexedPlan, _native, sol_attention_indexed
 from sol_testlib import HAS_GPU, assert_close
 
 gpu = pytest.mark.skipif(not HAS_GPU, reason="AMD ROCm GPU required")
@@ -47,7 +47,7 @@ CASES = [(3072, 3, 64, (1, 200), (0, 3072)),       # anchor rows over every key
 @pytest.mark.gpu
 @gpu
 @pytest.mark.parametrize("case", range(len(CASES)))
-def test_anchor_rows_match_the_dense_oracle_and_the_sol_path(case):
+def test_anchor_rows_match_the_dense_oracle_and_the_sol_path(case, monkeypatch):
     n, h, d, (w, nq), (a, b) = CASES[case]
     print(f"anchor rows case {case}: N{n} H{h} D{d} W{w} nq{nq} keys [{a}, {b})", flush=True)
     q, k, v = field(n, h, d, seed=80 + case)
@@ -58,9 +58,12 @@ def test_anchor_rows_match_the_dense_oracle_and_the_sol_path(case):
     got, stats = sol_attention_indexed(q, k, v, plan, beta=-math.inf, return_stats=True)
     assert got.shape == (w, nq, h, d)
     assert bool((stats.exact_blocks == -(-(b - a) // 64)).all())
-    # The SOL kernel's beta = -inf path over the same plan (pooled block tiles).
+    # The one-block SOL kernel's beta = -inf path over the same plan (pooled
+    # block tiles; the small-launch kernel's key split sums in other orders).
     sol_plan = dataclasses.replace(plan, key_range=None)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", 1)
     ref_sol = sol_attention_indexed(q, k, v, sol_plan, beta=-math.inf)
+    monkeypatch.setattr(_native, "WORKGROUP_FORM", 0)
     if (b - a) % 64 == 0:
         assert torch.equal(got, ref_sol)
     else:

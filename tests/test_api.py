@@ -145,7 +145,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == _native.ABI_VERSION == 11
+    assert native.sol_abi_version() == _native.ABI_VERSION == 12
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
@@ -242,10 +242,29 @@ def test_split_workspace_only_where_sinks_set_the_launch_end():
     assert size(1, 4096, 4096, 4, 128, -math.inf, 128) == 0   # every block exact
     assert size(1, 4096, 4096, 4, 128, 1.0, 64) == 0          # one sink block
     assert size(1, 4096, 4096, 4, 128, 1.0, 0) == 0           # no sinks
-    assert size(1, 1024, 1024, 8, 64, 1.0, 128) == 0          # 16 key blocks
+    assert size(1, 1024, 1024, 8, 64, 1.0, 128) == 0          # 16 key blocks (small-launch kernel)
     assert size(1, 84672, 84672, 24, 128, 1.0, 128) == 0      # many rounds of workgroups
     assert size(1, 4096, 4096, 4, 128, 1.0, 1100) == 0        # sinks over a quarter of the blocks
     assert size(1, 4096, 600000, 1, 128, 1.0, 128) == 0       # more than one routing segment
+
+
+def test_self_pooling_sizes_and_null_centroid_tiles():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.skip("libsol_attn_amd.so not built")
+    native = _native.library()
+    pools = native.sol_attention_pools_keys
+    assert pools(1, 1024, 1024, 8, 64) == 1 and pools(1, 1024, 1024, 8, 128) == 1
+    assert pools(1, 1024, 1025, 8, 64) == 0        # 17 key blocks: more than one pooling chunk
+    assert pools(1, 1024, 40, 8, 64) == 0          # fewer than 64 keys: pooled block tiles
+    assert pools(1, 4096, 1024, 16, 64) == 0       # 1,024 query blocks: not a small launch
+    assert pools(1, 1024, 1024, 8, 96) == 0        # unsupported head_dim
+    # NULL centroid tiles where the launch cannot pool its keys itself.
+    strides = (ctypes.c_int64 * 3)(64 * 8 * 4096, 64 * 8, 64)
+    fake = ctypes.c_void_p(1 << 20)
+    rc = native.sol_attention_fwd(fake, strides, None, 0, 1, 4096, 4096, None, 8, 64, fake, strides, fake, strides,
+                                  None, None, None, None, None, None, None, None, None, None, 0.125, 1.0, 1, 0, 0,
+                                  fake, None, None, None, None, None, None, None, 0, None)
+    assert rc == -1 and b"sol_attention_pools_keys" in native.sol_last_error()
 
 
 def test_noalloc_rejects_problems_beyond_its_workspace_without_launching():

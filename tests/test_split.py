@@ -26,9 +26,9 @@ pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not HAS_GPU, reason="AMD ROCm 
 
 # (batch, query tokens, key tokens, heads, head_dim, query sink tokens, inputs):
 # 64 query blocks x 4 heads with two sink blocks (4 parts of 16 key blocks);
-# three sink blocks (block 2 stays whole), tails, two parts, random inputs.
+# three sink blocks (block 2 stays whole), tails, four parts, random inputs.
 CASES = [(1, 4096, 4096, 4, 128, 128, "smooth"),
-         (2, 1000, 2500, 3, 64, 192, "random")]
+         (2, 1000, 5000, 3, 64, 192, "random")]
 
 
 def inputs(case):

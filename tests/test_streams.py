@@ -19,8 +19,8 @@ from sol_testlib import HAS_GPU, block_smooth
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not HAS_GPU, reason="AMD ROCm GPU required")]
 
 
-def inputs():
-    return [block_smooth(1, 2048, 4, 128, seed, device="cuda") for seed in (51, 52, 53)]
+def inputs(tokens=2048, heads=4, dim=128):
+    return [block_smooth(1, tokens, heads, dim, seed, device="cuda") for seed in (51, 52, 53)]
 
 
 def test_side_stream_matches_default_stream():
@@ -39,12 +39,24 @@ def test_side_stream_matches_default_stream():
 
 
 def _capture_cases():
-    """(name, setup(monkeypatch) -> call) for the launch shapes: the one-block
-    form; the two-block form with the pairing kernels (dynamic-LDS lag kernel
-    included); query sinks split by key range with the merge kernel; indexed
-    windows with the fused scatter into out=."""
+    """(name, setup(monkeypatch) -> call) for the launch shapes: the
+    small-launch kernel (key-split groups) after the pooling kernel, and as one
+    launch that pools its keys itself; the one-block form; the two-block form
+    with the pairing kernels (dynamic-LDS lag kernel included); query sinks
+    split by key range with the merge kernel; indexed windows with the fused
+    scatter into out=."""
+
+    def small(mp):
+        q, k, v = inputs()
+        return lambda: sol_attention(q, k, v, kv_sink_tokens=64)
+
+    def one_launch(mp):
+        q, k, v = inputs(1024, 8, 64)
+        assert _native.library().sol_attention_pools_keys(1, 1024, 1024, 8, 64) == 1
+        return lambda: sol_attention(q, k, v, kv_sink_tokens=128, query_sink_tokens=128)
 
     def plain(mp):
+        mp.setattr(_native, "WORKGROUP_FORM", 1)
         q, k, v = inputs()
         return lambda: sol_attention(q, k, v, kv_sink_tokens=64)
 
@@ -55,8 +67,8 @@ def _capture_cases():
         return lambda: sol_attention(q, k, v, kv_sink_tokens=64)
 
     def split(mp):
-        q, k, v = inputs()
-        assert _native.library().sol_split_workspace_size(1, 2048, 2048, 4, 128, 1.0, 128) > 0
+        q, k, v = inputs(4096)
+        assert _native.library().sol_split_workspace_size(1, 4096, 4096, 4, 128, 1.0, 128) > 0
         return lambda: sol_attention(q, k, v, kv_sink_tokens=64, query_sink_tokens=128)
 
     def indexed(mp):
@@ -67,7 +79,8 @@ def _capture_cases():
         out = torch.zeros_like(q)
         return lambda: sol_attention_indexed(q, k, v, plan, beta=1.0, out=out)
 
-    return {"one-block": plain, "paired": paired, "split-sinks": split, "indexed-scatter": indexed}
+    return {"small-launch": small, "one-launch": one_launch, "one-block": plain, "paired": paired,
+            "split-sinks": split, "indexed-scatter": indexed}
 
 
 @pytest.mark.parametrize("case", sorted(_capture_cases()))

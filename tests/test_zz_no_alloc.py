@@ -36,12 +36,14 @@ def _noalloc(q, k, v, beta, local, kv_sink, q_sink, out, counts):
 # (batch, query tokens, key tokens, heads, head_dim, beta, local, kv sink, q sink);
 # the second case is smaller than the first, the third exercises beta = -inf,
 # the fourth fewer keys than one block (block tiles in the workspace), the
-# fifth query sinks split by key range (split workspace in the scratch array).
+# fifth query sinks split by key range (split workspace in the scratch array),
+# the sixth one launch that pools its keys itself (no workspace at all).
 CASES = [(2, 4096, 4096, 16, 128, 1.0, 1, 128, 128),
          (1, 700, 1300, 3, 64, 0.5, 0, 64, 0),
          (1, 500, 900, 2, 128, -math.inf, 1, 0, 0),
          (1, 130, 40, 2, 64, 1.0, 1, 0, 0),
-         (1, 2048, 2048, 4, 128, 1.0, 1, 64, 128)]
+         (1, 4096, 4096, 4, 128, 1.0, 1, 64, 128),
+         (1, 1024, 1024, 8, 64, 1.0, 1, 128, 128)]
 
 
 def test_noalloc_matches_the_allocating_path_on_consecutive_calls():
@@ -65,7 +67,7 @@ import ctypes
 import torch
 from sol_attn_amd import _native
 from sol_testlib import block_smooth
-b, tq, tk, h, d = 1, 2048, 2048, 4, 128
+b, tq, tk, h, d = 1, 4096, 4096, 4, 128
 q = block_smooth(b, tq, h, d, seed=41, device="cuda")
 k = block_smooth(b, tk, h, d, seed=42, device="cuda")
 v = block_smooth(b, tk, h, d, seed=43, device="cuda")
