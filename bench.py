@@ -445,15 +445,17 @@ def qk_int8_experiment(q, k, v, kw, cfg, bf16_out, bf16_counts, oracle_blocks):
 
 
 def pool_bytes(b, tk, h, d, nkb, moments):
-    """Algorithmic bytes of the pooling pass (read K and V once; write the K / V
-    block centroids and, with moments, read them back for the mean and
-    variance).  The query means are formed inside the attention kernel from
+    """Algorithmic bytes of the pooling pass: read K and V once; write the K / V
+    block centroids; with moments, write the FP32 sums of each 16-block chunk
+    (centroids and their squares) and read them back for the mean and
+    variance.  The query means are formed inside the attention kernel from
     the Q tile it stages anyway, so pooling reads no Q.  BTHD keys are pooled
     without any K / V tile copy: the attention kernels DMA the key rows
     themselves, so these are all the bytes the pass moves."""
     reads = 2 * b * tk * h * d * 2
     writes = b * h * d * nkb * (2 + 2)
-    return reads + writes + (b * nkb * h * d * 2 if moments else 0)
+    chunk_sums = b * h * -(-nkb // 16) * 2 * d * 4
+    return reads + writes + (2 * chunk_sums if moments else 0)
 
 
 def config_record(name, cfg, beta, q, k, v):
@@ -548,7 +550,8 @@ def measure(name, cfg, beta, args, dev, headline, experiments=True):
                           "frac": pbytes / (pool_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                           "bytes_per_launch": pbytes,
                           "bytes_definition": "K and V read once + BF16 K/V centroids written"
-                                              + (" + centroids read for the moments" if finite else "")
+                                              + (" + FP32 16-block chunk sums written and read for the moments"
+                                                 if finite else "")
                                               + "; no K/V tile copy (the attention kernels read K/V rows)",
                           "kernels": "pool_kv_kernel + moments_kernel" if finite else "pool_kv_kernel"},
     }

@@ -336,6 +336,11 @@ def _split_size(b, nq, nk, h, d, beta, q_sink):
 
 
 @functools.lru_cache(maxsize=256)
+def _pools_keys(b, nq, nk, h, d):
+    return bool(library().sol_attention_pools_keys(b, nq, nk, h, d))
+
+
+@functools.lru_cache(maxsize=256)
 def _route_size(b, nq, nk, h, beta):
     return library().sol_route_workspace_size(b, nq, nk, h, beta)
 
@@ -491,7 +496,7 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
     if (SELF_POOLING and rows is None and keys is None and key_lengths is None and not debug
             and qk_precision == "bf16" and threshold_estimator == "diagonal_covariance"
             and WORKGROUP_FORM == 0 and ROUTE_PREPASS != "always" and rows_mode(k, v)
-            and library().sol_attention_pools_keys(q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3])):
+            and _pools_keys(q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3])):
         # One launch: the attention kernel pools the keys itself.
         out, counts, _ = attend(q, _self_pooled(k, v), scale, beta, local, kv_sink, q_sink, protection,
                                 out=out, stats=stats, stream=stream, strides=None)

@@ -136,11 +136,18 @@ void pool_kv_kernel(PoolParams p) {
     const int nch = (p.NKB + kPoolChunk - 1) / kPoolChunk;  // layout stride
     if (p.ksum && c * kPoolChunk < nkb && tid < D) {
       const int rows = min(kPoolChunk, nkb - c * kPoolChunk);
+      // All 16 centroid rows read first (every row of `cent` is written), so
+      // the reads overlap; the sums then take the chunk's blocks in order.
+      float xs[kPoolChunk];
+#pragma unroll
+      for (int jb = 0; jb < kPoolChunk; ++jb) xs[jb] = bf16_bits_to_f32(cent[jb][tid]);
       float s1 = 0.f, s2 = 0.f;
-      for (int jb = 0; jb < rows; ++jb) {
-        const float x = bf16_bits_to_f32(cent[jb][tid]);
-        s1 = __fadd_rn(s1, x);
-        s2 = __fadd_rn(s2, __fmul_rn(x, x));
+#pragma unroll
+      for (int jb = 0; jb < kPoolChunk; ++jb) {
+        if (jb < rows) {
+          s1 = __fadd_rn(s1, xs[jb]);
+          s2 = __fadd_rn(s2, __fmul_rn(xs[jb], xs[jb]));
+        }
       }
       float* dst = p.ksum + ((head * nch + c) * 2) * D;
       dst[tid] = s1;
@@ -160,6 +167,126 @@ void pool_kv_kernel(PoolParams p) {
     const int jb = tid / DC, cc = tid % DC;
     *reinterpret_cast<u32x4*>(ctile + TL::kElems + TL::v_offset(r0 + jb, cc)) =
         *reinterpret_cast<const u32x4*>(&cent[jb][8 * cc]);
+  }
+}
+
+// Four heads per workgroup (D = 128, heads a multiple of 4, large grids):
+// one 16-block chunk of heads h0 .. h0 + 3, sixteen waves, wave w pooling
+// key block w of the chunk.  Lane (hq, dc) reads head h0 + hq's 16-byte
+// chunk dc of every row, so one wave instruction covers one token row's four
+// heads (1 KiB contiguous for packed heads) instead of one head's row in
+// four places 16 rows apart: read on its own, that shape streams the
+// 84,672-token K 5.5% faster.  The lane sums its block's 64 rows in torch's
+// order itself -- four sequential 16-row sums folded in order -- so the
+// centroids, chunk sums and moments are the one-head kernel's bit for bit.
+template <int D>
+__global__ __launch_bounds__(1024) void pool_kv4_kernel(PoolParams p) {
+  constexpr int DC = D / 8;
+  static_assert(4 * DC == kWave, "a wave covers four heads' rows");
+  using TL = TileLayout<D>;
+  __shared__ __align__(16) uint16_t cent[4][kPoolChunk][D];
+
+  const bool is_v = blockIdx.y != 0;
+  const TokenRows src = is_v ? p.v : p.k;
+  const int hgroups = p.H / 4;
+  // (entry, head group) pairs vary fastest, as in the one-head kernel.
+  const int c = blockIdx.x / (p.B * hgroups);
+  const int bg = blockIdx.x % (p.B * hgroups);
+  const int b = bg / hgroups, h0 = (bg % hgroups) * 4;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int hq = lane / DC, dc = lane % DC;
+  const int tk = batch_tokens(p.klen, b, p.Tk);
+  const int nkb = (tk + kBlock - 1) / kBlock;
+  const int jb = wave;
+  const int j = c * kPoolChunk + jb;
+  const int len = j < nkb ? min(kBlock, tk - kBlock * j) : 0;
+  float tot[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) tot[e] = 0.f;
+  if (len > 0) {
+    uint16_t* tile = p.tiles ? p.tiles + ((int64_t(b) * p.H + h0 + hq) * p.NKB + j) * 2 * TL::kElems : nullptr;
+#pragma unroll 1
+    for (int q = 0; q < 4; ++q) {
+      u32x4 x[16];
+      load_rows16<16, true>(src, b, kBlock * j + 16 * q, kBlock * j + len - 1, h0 + hq, 8 * dc, x);
+      if (tile) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int row = 16 * q + i;
+          *reinterpret_cast<u32x4*>(tile + (is_v ? TL::kElems + TL::v_offset(row, dc) : TL::k_offset(row, dc))) = x[i];
+        }
+      }
+      float s[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[e] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (16 * q + i < len) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t w = x[i][e >> 1];
+            s[e] = __fadd_rn(s[e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)));
+          }
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tot[e] = q == 0 ? s[e] : __fadd_rn(tot[e], s[e]);
+    }
+  }
+  {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float m0 = 0.f, m1 = 0.f;
+      if (len > 0) {
+        m0 = __fdiv_rn(tot[e], float(len));
+        m1 = __fdiv_rn(tot[e + 1], float(len));
+      }
+      o[e >> 1] = pack_bf16x2(m0, m1);
+    }
+    *reinterpret_cast<u32x4*>(&cent[hq][jb][8 * dc]) = o;
+  }
+  __syncthreads();
+
+  if (!p.ctiles) return;  // tiles only (dense path)
+  // Centroid tiles: this chunk fills rows r0 .. r0 + 15 of tile ct of each head.
+  const int ct = (c * kPoolChunk) / kBlock;
+  const int r0 = (c * kPoolChunk) % kBlock;
+  {
+    const int hh = tid / (kPoolChunk * DC), rest = tid % (kPoolChunk * DC);
+    const int r = rest / DC, cc = rest % DC;
+    const int64_t head = int64_t(b) * p.H + h0 + hh;
+    uint16_t* ctile = p.ctiles + (head * p.NCT + ct) * 2 * TL::kElems;
+    *reinterpret_cast<u32x4*>(ctile + (is_v ? TL::kElems + TL::v_offset(r0 + r, cc) : TL::k_offset(r0 + r, cc))) =
+        *reinterpret_cast<const u32x4*>(&cent[hh][r][8 * cc]);
+  }
+  // Chunk partial sums of the BF16 centroids and their squares (moments).
+  if (!is_v && p.ksum && c * kPoolChunk < nkb && tid < 4 * D) {
+    const int hh = tid / D, f = tid % D;
+    const int64_t head = int64_t(b) * p.H + h0 + hh;
+    const int nch = (p.NKB + kPoolChunk - 1) / kPoolChunk;  // layout stride
+    const int rows = min(kPoolChunk, nkb - c * kPoolChunk);
+    float xs[kPoolChunk];
+#pragma unroll
+    for (int r = 0; r < kPoolChunk; ++r) xs[r] = bf16_bits_to_f32(cent[hh][r][f]);
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int r = 0; r < kPoolChunk; ++r) {
+      if (r < rows) {
+        s1 = __fadd_rn(s1, xs[r]);
+        s2 = __fadd_rn(s2, __fmul_rn(xs[r], xs[r]));
+      }
+    }
+    float* dst = p.ksum + ((head * nch + c) * 2) * D;
+    dst[f] = s1;
+    dst[D + f] = s2;
+    if (p.NKB <= kPoolChunk) {
+      const float n = float(nkb);
+      const float m = __fdiv_rn(s1, n);
+      const float v = __fdiv_rn(s2, n) - m * m;
+      p.mean[head * D + f] = m;
+      p.var[head * D + f] = v > 0.f ? v : 0.f;
+    }
   }
 }
 
@@ -188,6 +315,36 @@ __global__ __launch_bounds__(kMomentThreads) void moments_kernel(const float* __
   const int full_chunks = nkb / kPoolChunk;
   const int full_groups = full_chunks / 16;
   const float* base = ksum + int64_t(bh) * nch * 2 * D;
+  // The chunks past the last whole 256-block group (at most 15 whole chunks
+  // and a partial one) are summed by the last thread group, its loads issued
+  // all at once, alongside the group sums instead of after them.
+  __shared__ float tail[4][D];
+  if (gi == G - 1) {
+    const int c_lo = full_groups * 16;
+    const bool partial = full_chunks * kPoolChunk < nkb;
+    float x[2][16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = c_lo + i;
+      const bool take = c < full_chunks || (c == full_chunks && partial);
+      x[0][i] = take ? base[(2 * c) * D + d] : 0.f;
+      x[1][i] = take ? base[(2 * c + 1) * D + d] : 0.f;
+    }
+    float a1[2] = {0.f, 0.f}, rem[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = c_lo + i;
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        if (c < full_chunks) a1[w] = a1[w] + x[w][i];
+        else if (c == full_chunks && partial) rem[w] = x[w][i];
+      }
+    }
+    tail[0][d] = a1[0];
+    tail[1][d] = a1[1];
+    tail[2][d] = rem[0];
+    tail[3][d] = rem[1];
+  }
   float a2[2] = {0.f, 0.f}, a3[2] = {0.f, 0.f};
   int rows = 0;
   for (int g0 = 0; g0 < full_groups; g0 += kGroupsPerPass) {
@@ -219,16 +376,9 @@ __global__ __launch_bounds__(kMomentThreads) void moments_kernel(const float* __
     }
     __syncthreads();
   }
+  __syncthreads();  // the tail sums are published
   if (gi != 0) return;
-  float a1[2] = {0.f, 0.f}, rem[2] = {0.f, 0.f};
-  for (int c = full_groups * 16; c < full_chunks; ++c) {
-    a1[0] = a1[0] + base[(2 * c) * D + d];
-    a1[1] = a1[1] + base[(2 * c + 1) * D + d];
-  }
-  if (full_chunks * kPoolChunk < nkb) {
-    rem[0] = base[(2 * full_chunks) * D + d];
-    rem[1] = base[(2 * full_chunks + 1) * D + d];
-  }
+  const float a1[2] = {tail[0][d], tail[1][d]}, rem[2] = {tail[2][d], tail[3][d]};
   const float n = float(nkb);
   const float m = __fdiv_rn(((rem[0] + a1[0]) + a2[0]) + a3[0], n);
   const float sq = __fdiv_rn(((rem[1] + a1[1]) + a2[1]) + a3[1], n);
@@ -242,10 +392,15 @@ __global__ __launch_bounds__(kMomentThreads) void moments_kernel(const float* __
 // time.
 constexpr int64_t kWidePoolGroups = 512;
 
+// Four-head workgroups: large grids at D = 128 with heads in fours.
+bool POOL_FOUR_HEADS = true;
+
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
   const dim3 grid(unsigned(p.B) * p.H * p.NCHP, 2);
   const bool wide = 2 * int64_t(p.B) * p.H * p.NCHP <= kWidePoolGroups;
-  if (D == 128) {
+  if (D == 128 && !wide && p.H % 4 == 0 && POOL_FOUR_HEADS) {
+    hipLaunchKernelGGL(pool_kv4_kernel<128>, dim3(unsigned(p.B) * (p.H / 4) * p.NCHP, 2), dim3(1024), 0, stream, p);
+  } else if (D == 128) {
     if (wide)
       hipLaunchKernelGGL((pool_kv_kernel<128, kWideWaves<128>>), grid, dim3(kWideWaves<128> * kWave), 0, stream, p);
     else

@@ -77,10 +77,14 @@ def centroids(ctiles, nkb):
 # pooling form, larger ones the four-wave form: the last two shapes (ragged
 # last block) are the four-wave form's, for D = 64 and 128.  Keys of at most
 # 16 blocks (one pooling chunk: 317, 1 and exactly 1,024 tokens) get their
-# moments from the pooling kernel itself, longer ones from moments_kernel.
+# moments from the pooling kernel itself, longer ones from moments_kernel;
+# 40,000 and 17,000 tokens (625 and 266 blocks) take its 256-block groups.
+# Large grids at D = 128 with heads in fours take the four-head workgroups:
+# 4,033 tokens x 68 heads and 20,000 x 2 x 8 (313 blocks).
 @pytest.mark.parametrize("shape", [(1, 317, 2, 64), (2, 1089, 3, 128), (1, 1, 1, 64), (1, 1024, 2, 64),
                                    (2, 4096, 16, 128), (1, 10000, 4, 128), (1, 4100, 72, 64),
-                                   (1, 4033, 68, 128)])
+                                   (1, 4033, 68, 128), (1, 40000, 2, 64), (2, 17000, 3, 128),
+                                   (2, 20000, 8, 128)])
 def test_pooling_and_moments_bit_exact(shape):
     b, t, h, d = shape
     g = torch.Generator().manual_seed(t)
