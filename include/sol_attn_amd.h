@@ -229,8 +229,8 @@ int64_t sol_route_workspace_size(int64_t batch, int64_t query_tokens, int64_t ke
  * sol_pool_kv wrote, and k / v are ignored (may be NULL). */
 /* 1 when sol_attention_fwd over plain K / V rows of these sizes pools the
  * keys inside its one attention launch (ctiles, key_mean and key_var may be
- * NULL): at least 64 and at most 1,024 keys (one pooling chunk of 16
- * blocks) in a launch of the small-launch kernel (workgroup_form).  0
+ * NULL): head_dim 64, at least 64 and at most 1,024 keys (one pooling chunk
+ * of 16 blocks) in a launch of the small-launch kernel (workgroup_form).  0
  * otherwise.  No counterpart in the reference: it launches `_pool`,
  * `_moments`, `_threshold` and `_sol` separately (kernels.py:203-225). */
 int sol_attention_pools_keys(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,

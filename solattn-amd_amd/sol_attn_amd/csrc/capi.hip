@@ -127,10 +127,15 @@ int sink_splits(int64_t bh, int64_t nqb, int64_t nkb, int64_t q_sink_blocks, int
 }
 
 // Whether a launch of these sizes over plain K / V rows runs as one kernel
-// that pools the keys itself (sol_attention_pools_keys).
+// that pools the keys itself (sol_attention_pools_keys).  Head_dim 64 only:
+// every workgroup reads its head's whole K and V to pool them, which the
+// four two-wave groups at head_dim 64 absorb (1,024 tokens x 8 heads: 19.1
+// us against 23.3 for the pooling kernel + small kernel); at head_dim 128
+// the two groups read twice the bytes and lose (33.3 against 24.6 us at
+// 1,024 tokens x 4 heads).
 bool pools_keys(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads, int64_t head_dim) {
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
-  return key_tokens >= SOL_BLOCK && nkb <= sol::kPoolChunk &&
+  return head_dim == 64 && key_tokens >= SOL_BLOCK && nkb <= sol::kPoolChunk &&
          sol::small_key_split(batch * heads * cdiv(query_tokens, SOL_BLOCK), nkb, head_dim) > 0;
 }
 

@@ -253,7 +253,8 @@ def test_self_pooling_sizes_and_null_centroid_tiles():
         pytest.skip("libsol_attn_amd.so not built")
     native = _native.library()
     pools = native.sol_attention_pools_keys
-    assert pools(1, 1024, 1024, 8, 64) == 1 and pools(1, 1024, 1024, 8, 128) == 1
+    assert pools(1, 1024, 1024, 8, 64) == 1
+    assert pools(1, 1024, 1024, 8, 128) == 0       # head_dim 128: the pooling kernel first
     assert pools(1, 1024, 1025, 8, 64) == 0        # 17 key blocks: more than one pooling chunk
     assert pools(1, 1024, 40, 8, 64) == 0          # fewer than 64 keys: pooled block tiles
     assert pools(1, 4096, 1024, 16, 64) == 0       # 1,024 query blocks: not a small launch
