@@ -539,6 +539,7 @@ def measure(name, cfg, beta, args, dev, headline, experiments=True):
         "roofline": {"bound": "mfma", "achieved": attn_tflops, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": attn_tflops / PEAK_BF16_TFLOPS,
                      "traffic": traffic["traffic_bytes"] if traffic else None,
+                     "l2_hit_rate": traffic.get("l2_hit_rate") if traffic else None,
                      "traffic_source": (f"{traffic['source']} ({traffic['kernel']}: rocprofv3 FETCH_SIZE x "
                                         f"{traffic['fetch_scale']} + WRITE_SIZE x {traffic['write_scale']}, "
                                         f"scaled by a 1 GiB copy)") if traffic else None,
