@@ -648,10 +648,11 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
       const float qm = s_qm[qg][lt];
       a = qm * p.mean[head * D + lt];
       if (p.cov) {
-        // Full covariance: this feature's term of Qc^T cov Qc.
-        const float* row = p.cov + (head * D + lt) * D;
+        // Full covariance: this feature's term of Qc^T cov Qc.  cov is
+        // symmetric bit for bit, so thread lt reads column lt (coalesced).
+        const float* col = p.cov + int64_t(head) * D * D + lt;
         float sq = 0.f;
-        for (int e = 0; e < D; ++e) sq = fmaf(row[e], s_qm[qg][e], sq);
+        for (int e = 0; e < D; ++e) sq = fmaf(col[e * D], s_qm[qg][e], sq);
         g = qm * sq;
       } else {
         g = qm * qm * p.var[head * D + lt];
@@ -1067,9 +1068,9 @@ __global__ __launch_bounds__(128 * KS, KS / 2) void sol_small_kernel(AttnParams 
       const float mu = POOL ? s_mom[0][tid] : p.mean[head * D + tid];
       a = qm * mu;
       if (p.cov) {
-        const float* row = p.cov + (head * D + tid) * D;
+        const float* col = p.cov + int64_t(head) * D * D + tid;  // symmetric: column tid
         float sq = 0.f;
-        for (int e = 0; e < D; ++e) sq = fmaf(row[e], s_qm[e], sq);
+        for (int e = 0; e < D; ++e) sq = fmaf(col[e * D], s_qm[e], sq);
         g = qm * sq;
       } else {
         g = qm * qm * (POOL ? s_mom[1][tid] : p.var[head * D + tid]);

@@ -151,20 +151,29 @@ __global__ __launch_bounds__(kRouteThreads, 2) void route_kernel(AttnParams p) {
         }
       }
     if (p.cov) {
-      // Full covariance (experiment): this feature's term of Qc^T cov Qc.
+      // Full covariance (experiment): this feature's term of Qc^T cov Qc,
+      // sum_e cov[d][e] Qc_e in feature order.  cov is symmetric bit for bit
+      // (covariance_partial_kernel forms entry (d, e) and (e, d) by the same
+      // fmas in the same order), so lane d reads column d: one coalesced load
+      // per feature e serves the wave's BW blocks.
 #pragma unroll
-      for (int i = 0; i < BW; ++i)
+      for (int part = 0; part < 2; ++part) {
+        const int d = 64 * part + lane;
+        if (d < D) {
+          float sq[BW];
 #pragma unroll
-        for (int part = 0; part < 2; ++part) {
-          const int jb = wave * BW + i, d = 64 * part + lane;
-          if (d < D) {
-            const float* row = p.cov + (head * D + d) * D;
-            float sq = 0.f;
-#pragma unroll 1
-            for (int e = 0; e < D; ++e) sq = fmaf(row[e], s_qc[jb][e], sq);
-            g[i][part] = s_qc[jb][d] * sq;
+          for (int i = 0; i < BW; ++i) sq[i] = 0.f;
+          const float* col = p.cov + int64_t(head) * D * D + d;
+#pragma unroll 4
+          for (int e = 0; e < D; ++e) {
+            const float c = col[e * D];
+#pragma unroll
+            for (int i = 0; i < BW; ++i) sq[i] = fmaf(c, s_qc[wave * BW + i][e], sq[i]);
           }
+#pragma unroll
+          for (int i = 0; i < BW; ++i) g[i][part] = s_qc[wave * BW + i][d] * sq[i];
         }
+      }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1)

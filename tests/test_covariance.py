@@ -1,7 +1,7 @@
 """Full-covariance thresholds (the reference roadmap's experiment; not in the reference).
 
 GPU: the key covariance (sol_key_covariance) against the oracle's float64
-estimator; routing decisions, cutoffs and outputs against the oracle under
+estimator, and its exact symmetry; routing decisions, cutoffs and outputs against the oracle under
 the full-covariance cutoff (the same band and tolerances as the diagonal
 path); beta = 0 makes both estimators identical; ragged indexed windows.
 """
@@ -39,6 +39,8 @@ def test_key_covariance_matches_oracle(shape):
     kc = orc.block_means(to_np(k), True)
     ref = orc.key_covariance(kc)
     np.testing.assert_allclose(cov, ref, rtol=0, atol=2e-6 * np.abs(ref).max() + 1e-7)
+    # Symmetric bit for bit: the cutoff stages read column d for row d.
+    np.testing.assert_array_equal(cov, np.swapaxes(cov, -1, -2))
     # Its diagonal is the diagonal estimator's variance before the clamp.
     _, var = orc.key_moments(kc)
     diag = np.diagonal(cov, axis1=-2, axis2=-1)
