@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 12
+#define SOL_ABI_VERSION 13
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_TOKENS (1ll << 25) /* key_tokens of one pooling call (2^19 key blocks) */
 
@@ -308,6 +308,41 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides,
                   int64_t batch, int64_t query_tokens, int64_t key_tokens,
                   int64_t heads, int64_t head_dim, double scale,
                   void* tiles, void* out, const int64_t* out_index, void* stream);
+
+/* Bytes of caller workspace sol_attention_all_in needs for these sizes: 0
+ * when the attention launch pools its keys itself (sol_attention_pools_keys),
+ * otherwise the sol_pool_kv buffers it uses, each 256-byte aligned (the
+ * centroid tiles; the block tiles outside rows mode, which k_token_stride /
+ * v_token_stride -- K's and V's token strides in elements -- and key_tokens
+ * decide as in sol_attention_fwd; chunk sums and moments at finite beta) and
+ * the split workspace (sol_split_workspace_size).  -1 for invalid sizes.
+ * No counterpart in the reference. */
+int64_t sol_attention_workspace_size(int64_t batch, int64_t query_tokens, int64_t key_tokens,
+                                     int64_t heads, int64_t head_dim, double beta,
+                                     int64_t query_sink_tokens, int64_t k_token_stride,
+                                     int64_t v_token_stride);
+
+/* All-in SOL attention in one call: sol_pool_kv followed by
+ * sol_attention_fwd over BTHD inputs (no index, plan protection, covariance,
+ * INT8 tiles or debug outputs; routing inside the attention kernel; one
+ * launch when sol_attention_pools_keys holds), with the pooled key buffers
+ * carved from `workspace` (sol_attention_workspace_size bytes, 16-byte
+ * aligned; NULL when that size is 0).  Replaces the two calls of the launch
+ * layer's `_sol` path (src/sol_attn_amd/kernels.py:203-225: pooling, moments,
+ * threshold and `_sol`) for launches that need no query-block pairing: it
+ * saves the host one call and its argument packing, which short launches
+ * (tens of microseconds of GPU work) feel.  Results are bit-identical to
+ * sol_pool_kv + sol_attention_fwd with the same workspace layout.  out:
+ * contiguous BF16 [batch, query_tokens, heads, head_dim]; counts: NULL or
+ * int32 [batch, NQB, heads]; other arguments as in sol_attention_fwd. */
+int sol_attention_all_in(const void* q, const int64_t* q_strides,
+                         const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides,
+                         int64_t batch, int64_t query_tokens, int64_t key_tokens,
+                         int64_t heads, int64_t head_dim, double scale, double beta,
+                         int64_t local_blocks, int64_t kv_sink_tokens,
+                         int64_t query_sink_tokens, void* workspace, int64_t workspace_bytes,
+                         void* out, int32_t* counts, void* stream);
 
 /* All-in SOL attention that allocates nothing: sol_pool_kv followed by
  * sol_attention_fwd (BTHD inputs; no index, plan protection, covariance or

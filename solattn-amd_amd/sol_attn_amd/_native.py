@@ -18,7 +18,7 @@ import threading
 import torch
 
 BLOCK = 64
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")
@@ -54,6 +54,9 @@ _SIGNATURES = {
     "sol_attention_pools_keys": ([_i64, _i64, _i64, _i64, _i64], ctypes.c_int),
     "sol_attention_noalloc": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
                                _dbl, _dbl, _i64, _i64, _i64, _p, _p, _p], ctypes.c_int),
+    "sol_attention_workspace_size": ([_i64, _i64, _i64, _i64, _i64, _dbl, _i64, _i64, _i64], ctypes.c_int64),
+    "sol_attention_all_in": ([_p, _i64p, _p, _i64p, _p, _i64p, _i64, _i64, _i64, _i64, _i64,
+                              _dbl, _dbl, _i64, _i64, _i64, _p, _i64, _p, _p, _p], ctypes.c_int),
 }
 
 
@@ -451,6 +454,36 @@ def attend(q, pooled, scale, beta, local, kv_sink, q_sink, protection=None, rows
 # way (the same centroids and moments, bit for bit).
 SELF_POOLING = True
 
+# Plain BTHD calls that need no query-block pairing go through one C-ABI call,
+# sol_attention_all_in (pooling + attention, the pooled key buffers carved
+# from one workspace), instead of sol_pool_kv + sol_attention_fwd: the same
+# kernels and workspace layout, bit-identical results, and one call's host
+# cost fewer.  False keeps the two calls.
+ALL_IN = True
+
+
+@functools.lru_cache(maxsize=256)
+def _all_in_size(b, nq, nk, h, d, beta, q_sink, k_stride, v_stride):
+    return library().sol_attention_workspace_size(b, nq, nk, h, d, beta, q_sink, k_stride, v_stride)
+
+
+def _all_in(q, k, v, scale, beta, local, kv_sink, q_sink, stats):
+    """``(out, counts)`` of one sol_attention_all_in call (BTHD, the caller's stream)."""
+    q, k, v = _rows(q), _rows(k), _rows(v)
+    b, nq, h, d = q.shape
+    nk = k.shape[1]
+    dev = q.device
+    size = _all_in_size(b, nq, nk, h, d, beta, q_sink, k.stride(1), v.stride(1))
+    if size < 0:
+        raise RuntimeError("sol_attention_workspace_size rejected the sizes")
+    ws = torch.empty(size, device=dev, dtype=torch.uint8) if size else None
+    out = torch.empty((b, nq, h, d), device=dev, dtype=torch.bfloat16)
+    counts = torch.empty((b, -(-nq // BLOCK), h), device=dev, dtype=torch.int32) if stats else None
+    _check(library().sol_attention_all_in(
+        q.data_ptr(), _strides(q), k.data_ptr(), _strides(k), v.data_ptr(), _strides(v), b, nq, nk, h, d,
+        scale, beta, local, kv_sink, q_sink, _ptr(ws), size, out.data_ptr(), _ptr(counts), _stream(dev)))
+    return out, counts
+
 
 def _self_pooled(k, v):
     """The ``pool_kv`` record of keys the attention launch pools itself: plain
@@ -492,10 +525,15 @@ def launch_sol(q, k, v, scale, beta, local, kv_sink, q_sink, stats, protection=N
         if stats:
             counts = torch.full((b, -(-nq // BLOCK), h), -(-k.shape[1] // BLOCK), device=q.device, dtype=torch.int32)
         return dense, counts
+    plain = (rows is None and keys is None and key_lengths is None and not debug and qk_precision == "bf16"
+             and threshold_estimator == "diagonal_covariance" and WORKGROUP_FORM == 0
+             and ROUTE_PREPASS != "always")
+    if (ALL_IN and plain and protection is None and out is None and SELF_POOLING and SPLIT_SINKS
+            and (not PAIRING or q.shape[0] * q.shape[2] * -(-q.shape[1] // BLOCK) < PAIR_MIN_QUERY_BLOCKS)):
+        # No pairing pass: pooling and attention in one C-ABI call.
+        return _all_in(q, k, v, float(scale), float(beta), int(local), int(kv_sink), int(q_sink), stats)
     stream = _stream(q.device)
-    if (SELF_POOLING and rows is None and keys is None and key_lengths is None and not debug
-            and qk_precision == "bf16" and threshold_estimator == "diagonal_covariance"
-            and WORKGROUP_FORM == 0 and ROUTE_PREPASS != "always" and rows_mode(k, v)
+    if (SELF_POOLING and plain and rows_mode(k, v)
             and _pools_keys(q.shape[0], q.shape[1], k.shape[1], q.shape[2], q.shape[3])):
         # One launch: the attention kernel pools the keys itself.
         out, counts, _ = attend(q, _self_pooled(k, v), scale, beta, local, kv_sink, q_sink, protection,

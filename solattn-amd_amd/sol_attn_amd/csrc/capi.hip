@@ -569,60 +569,135 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides, const int64_t* query_
   return hip_status(sol::launch_dense(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
+}  // extern "C"
+
+namespace {
+
+// Byte layout of the all-in workspace: the sol_pool_kv buffers, 256-byte
+// aligned, in the order sol_pool_sizes lists them (the block tiles only
+// outside rows mode, the moment buffers only at finite beta), then the split
+// workspace.  total 0: the launch pools its keys itself and needs none.
+struct AllInLayout {
+  bool rows, moments, self_pooled;
+  int64_t tiles, sums, mean, var, split, split_bytes, total;
+};
+
+AllInLayout all_in_layout(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                          int64_t head_dim, double beta, int64_t query_sink_tokens, bool rows) {
+  AllInLayout l{};
+  l.rows = rows;
+  l.moments = std::isfinite(beta);
+  l.self_pooled = rows && !(std::isinf(beta) && beta < 0) &&
+                  pools_keys(batch, query_tokens, key_tokens, heads, head_dim);
+  if (l.self_pooled) return l;
+  int64_t sizes[4];
+  sol_pool_sizes(batch, key_tokens, heads, head_dim, sizes);
+  l.tiles = align256(sizes[0]);
+  l.sums = l.tiles + (rows ? 0 : align256(sizes[1]));
+  l.mean = l.sums + align256(sizes[2]);
+  l.var = l.mean + align256(sizes[3]);
+  l.split = l.moments ? l.var + align256(sizes[3]) : l.sums;
+  l.split_bytes = sol_split_workspace_size(batch, query_tokens, key_tokens, heads, head_dim, beta,
+                                           query_sink_tokens);
+  l.total = l.split + align256(l.split_bytes);
+  return l;
+}
+
+// Pooling + attention over BTHD inputs in workspace `ws` (`ws_bytes` bytes;
+// NULL / 0 when the launch pools its keys itself).  `scratch`: the workspace
+// is the library's device array (sol_attention_noalloc), looked up only after
+// every check has passed, and `ws` is ignored.
+int all_in(const char* who, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+           const void* v, const int64_t* v_strides, int64_t batch, int64_t query_tokens, int64_t key_tokens,
+           int64_t heads, int64_t head_dim, double scale, double beta, int64_t local_blocks,
+           int64_t kv_sink_tokens, int64_t query_sink_tokens, uint8_t* ws, int64_t ws_bytes, bool scratch,
+           void* out, int32_t* counts, void* stream) {
+  static thread_local std::string msg;
+  if (!shape_ok(batch, query_tokens, heads, head_dim) || !shape_ok(batch, key_tokens, heads, head_dim) ||
+      key_tokens >= (int64_t(1) << 30)) {
+    msg = std::string(who) + ": unsupported shape (head_dim must be 64 or 128)";
+    return fail(SOL_ERR_INVALID, msg.c_str());
+  }
+  const int arc = attention_args_ok(who, q, q_strides, false, batch, query_tokens, heads, scale, beta,
+                                    kv_sink_tokens, query_sink_tokens, out);
+  if (arc != SOL_OK) return arc;
+  const bool rows = rows_mode_possible(nullptr, nullptr, key_tokens, k_strides, v_strides);
+  const AllInLayout l = all_in_layout(batch, query_tokens, key_tokens, heads, head_dim, beta, query_sink_tokens,
+                                      rows);
+  // One attention launch that pools the keys itself: no workspace at all.
+  if (l.self_pooled)
+    return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads, head_dim,
+                             k, k_strides, v, v_strides, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                             nullptr, nullptr, nullptr, nullptr, scale, beta, local_blocks, kv_sink_tokens,
+                             query_sink_tokens, out, nullptr, counts, nullptr, nullptr, nullptr, nullptr, nullptr,
+                             0, stream);
+  if (l.total > ws_bytes) {
+    msg = scratch ? std::string(who) +
+                        ": the pooled keys need more than SOL_NOALLOC_SCRATCH_BYTES (128 MiB); use "
+                        "sol_attention_all_in or sol_pool_kv + sol_attention_fwd with caller workspace"
+                  : std::string(who) + ": workspace_bytes is below sol_attention_workspace_size";
+    return fail(scratch ? SOL_ERR_UNSUPPORTED : SOL_ERR_INVALID, msg.c_str());
+  }
+  if (scratch) {
+    void* base = nullptr;
+    const int rc = scratch_on_current_device(&base);
+    if (rc != SOL_OK) return rc;
+    ws = static_cast<uint8_t*>(base);
+  } else if (!aligned16(ws)) {
+    msg = std::string(who) + ": workspace must be a 16-byte aligned device buffer";
+    return fail(SOL_ERR_INVALID, msg.c_str());
+  }
+  float* sums = l.moments ? reinterpret_cast<float*>(ws + l.sums) : nullptr;
+  float* mean = l.moments ? reinterpret_cast<float*>(ws + l.mean) : nullptr;
+  float* var = l.moments ? reinterpret_cast<float*>(ws + l.var) : nullptr;
+  void* tiles = rows ? nullptr : ws + l.tiles;
+  const int prc = pool_checked(who, k, k_strides, v, v_strides, nullptr, nullptr, 0, batch, key_tokens, heads,
+                               head_dim, ws, tiles, sums, mean, var, stream);
+  if (prc != SOL_OK) return prc;
+  return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
+                           head_dim, k, k_strides, v, v_strides, tiles, ws, mean, var, nullptr, nullptr, nullptr,
+                           l.split_bytes ? ws + l.split : nullptr, nullptr /* routing in the attention kernel */,
+                           nullptr, scale, beta, local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr,
+                           counts, nullptr, nullptr, nullptr, nullptr, nullptr, 0, stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t sol_attention_workspace_size(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
+                                     int64_t head_dim, double beta, int64_t query_sink_tokens,
+                                     int64_t k_token_stride, int64_t v_token_stride) {
+  if (!shape_ok(batch, query_tokens, heads, head_dim) || !shape_ok(batch, key_tokens, heads, head_dim) ||
+      key_tokens >= (int64_t(1) << 30) || query_sink_tokens < 0 || std::isnan(beta) || k_token_stride <= 0 ||
+      v_token_stride <= 0)
+    return -1;
+  const int64_t ks[3] = {0, k_token_stride, 1}, vs[3] = {0, v_token_stride, 1};
+  const bool rows = rows_mode_possible(nullptr, nullptr, key_tokens, ks, vs);
+  return all_in_layout(batch, query_tokens, key_tokens, heads, head_dim, beta, query_sink_tokens, rows).total;
+}
+
+int sol_attention_all_in(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides, int64_t batch, int64_t query_tokens,
+                         int64_t key_tokens, int64_t heads, int64_t head_dim, double scale, double beta,
+                         int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens, void* workspace,
+                         int64_t workspace_bytes, void* out, int32_t* counts, void* stream) {
+  if (workspace_bytes < 0 || (workspace_bytes > 0 && !workspace))
+    return fail(SOL_ERR_INVALID, "sol_attention_all_in: workspace_bytes must be >= 0, with a workspace if > 0");
+  return all_in("sol_attention_all_in", q, q_strides, k, k_strides, v, v_strides, batch, query_tokens, key_tokens,
+                heads, head_dim, scale, beta, local_blocks, kv_sink_tokens, query_sink_tokens,
+                static_cast<uint8_t*>(workspace), workspace_bytes, false, out, counts, stream);
+}
+
 int sol_attention_noalloc(const void* q, const int64_t* q_strides, const void* k,
                           const int64_t* k_strides, const void* v, const int64_t* v_strides,
                           int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
                           int64_t head_dim, double scale, double beta, int64_t local_blocks,
                           int64_t kv_sink_tokens, int64_t query_sink_tokens, void* out,
                           int32_t* counts, void* stream) {
-  if (!shape_ok(batch, query_tokens, heads, head_dim) || !shape_ok(batch, key_tokens, heads, head_dim))
-    return fail(SOL_ERR_INVALID, "sol_attention_noalloc: unsupported shape (head_dim must be 64 or 128)");
-  const int arc = attention_args_ok("sol_attention_noalloc", q, q_strides, false, batch, query_tokens, heads,
-                                    scale, beta, kv_sink_tokens, query_sink_tokens, out);
-  if (arc != SOL_OK) return arc;
-  const bool rows = rows_mode_possible(nullptr, nullptr, key_tokens, k_strides, v_strides);
-  // One attention launch that pools the keys itself: no workspace at all.
-  if (rows && !(std::isinf(beta) && beta < 0) && pools_keys(batch, query_tokens, key_tokens, heads, head_dim))
-    return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads, head_dim,
-                             k, k_strides, v, v_strides, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
-                             nullptr, nullptr, nullptr, nullptr, scale, beta, local_blocks, kv_sink_tokens,
-                             query_sink_tokens, out, nullptr, counts, nullptr, nullptr, nullptr, nullptr, nullptr,
-                             0, stream);
-  // The sol_pool_kv buffers, 256-byte aligned, in the order sol_pool_sizes lists them.
-  int64_t sizes[4];
-  if (sol_pool_sizes(batch, key_tokens, heads, head_dim, sizes) != SOL_OK) return SOL_ERR_INVALID;
-  const bool moments = std::isfinite(beta);
-  // Rows mode needs no block tiles; fewer than 64 keys (or huge token
-  // strides) take them in the workspace.
-  const int64_t off_tiles = align256(sizes[0]);
-  const int64_t off_sums = off_tiles + (rows ? 0 : align256(sizes[1]));
-  const int64_t off_mean = off_sums + align256(sizes[2]);
-  const int64_t off_var = off_mean + align256(sizes[3]);
-  const int64_t off_split = moments ? off_var + align256(sizes[3]) : off_sums;
-  const int64_t split = sol_split_workspace_size(batch, query_tokens, key_tokens, heads, head_dim, beta,
-                                                 query_sink_tokens);
-  const int64_t need = off_split + align256(split);
-  if (need > SOL_NOALLOC_SCRATCH_BYTES)
-    return fail(SOL_ERR_UNSUPPORTED,
-                "sol_attention_noalloc: the pooled keys need more than SOL_NOALLOC_SCRATCH_BYTES "
-                "(128 MiB); use sol_pool_kv + sol_attention_fwd with caller workspace");
-  void* base = nullptr;
-  const int rc = scratch_on_current_device(&base);
-  if (rc != SOL_OK) return rc;
-  uint8_t* ws = static_cast<uint8_t*>(base);
-  float* sums = moments ? reinterpret_cast<float*>(ws + off_sums) : nullptr;
-  float* mean = moments ? reinterpret_cast<float*>(ws + off_mean) : nullptr;
-  float* var = moments ? reinterpret_cast<float*>(ws + off_var) : nullptr;
-  void* tiles = rows ? nullptr : ws + off_tiles;
-  const int prc = pool_checked("sol_attention_noalloc", k, k_strides, v, v_strides, nullptr, nullptr, 0, batch,
-                               key_tokens, heads, head_dim, ws, tiles, sums, mean, var, stream);
-  if (prc != SOL_OK) return prc;
-  return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
-                           head_dim, k, k_strides, v, v_strides, tiles, ws, mean, var, nullptr, nullptr, nullptr,
-                           split ? ws + off_split : nullptr, nullptr /* routing in the attention kernel */,
-                           nullptr, scale, beta,
-                           local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr, counts, nullptr,
-                           nullptr, nullptr, nullptr, nullptr, 0, stream);
+  return all_in("sol_attention_noalloc", q, q_strides, k, k_strides, v, v_strides, batch, query_tokens, key_tokens,
+                heads, head_dim, scale, beta, local_blocks, kv_sink_tokens, query_sink_tokens, nullptr,
+                SOL_NOALLOC_SCRATCH_BYTES, true, out, counts, stream);
 }
 
 }  // extern "C"

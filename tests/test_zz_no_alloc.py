@@ -1,7 +1,8 @@
 """The allocation-free entry point (sol_attention_noalloc), called through the
 C-ABI, against the allocating path (sol_pool_kv + sol_attention_fwd through
-_native.launch_sol): bit-identical outputs and exact-block counts on two calls
-in a row, the second smaller, so the shared device workspace is reused."""
+_native.launch_sol, as two calls): bit-identical outputs and exact-block
+counts on two calls in a row, the second smaller, so the shared device
+workspace is reused."""
 
 import ctypes
 import math
@@ -46,7 +47,10 @@ CASES = [(2, 4096, 4096, 16, 128, 1.0, 1, 128, 128),
          (1, 1024, 1024, 8, 64, 1.0, 1, 128, 128)]
 
 
-def test_noalloc_matches_the_allocating_path_on_consecutive_calls():
+def test_noalloc_matches_the_allocating_path_on_consecutive_calls(monkeypatch):
+    # The reference path as two C-ABI calls (not sol_attention_all_in, which
+    # shares the noalloc entry point's code).
+    monkeypatch.setattr(_native, "ALL_IN", False)
     for i, (b, tq, tk, h, d, beta, local, kvs, qs) in enumerate(CASES):
         print(f"case {i}: B{b} Tq{tq} Tk{tk} H{h} D{d} beta {beta}", flush=True)
         q = block_smooth(b, tq, h, d, seed=10 + i, device="cuda")
@@ -80,6 +84,7 @@ rc = lib.sol_attention_noalloc(q.data_ptr(), st(q), k.data_ptr(), st(k), v.data_
                                torch.cuda.current_stream().cuda_stream)
 assert rc == 0, lib.sol_last_error().decode()
 torch.cuda.synchronize()
+_native.ALL_IN = False
 ref, _ = _native.launch_sol(q, k, v, d ** -0.5, 1.0, 1, 64, 128, False)
 assert torch.equal(out, ref)
 print("first-call noalloc ok", flush=True)
