@@ -196,6 +196,26 @@ int attention_args_ok(const char* who, const void* q, const int64_t* q_strides, 
   return SOL_OK;
 }
 
+// sol_attention_fwd with, at finite beta, the pooling pass's chunk sums in
+// place of key_mean / key_var (chunk_sums non-null: the cutoff stage folds
+// the moments itself; folds_moments key sequences, no key_lengths, no
+// route_workspace or key_cov).
+int attention_fwd_impl(const void* q, const int64_t* q_strides, const int64_t* query_index,
+                      int64_t sequence_length, int64_t batch, int64_t query_tokens,
+                      int64_t key_tokens,
+                      const int32_t* key_lengths, int64_t heads, int64_t head_dim,
+                      const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                      const void* tiles, const void* ctiles, const float* key_mean,
+                      const float* key_var, const float* key_cov, const uint8_t* protection,
+                      const int32_t* pair_strides, void* split_workspace, void* route_workspace,
+                      const float* query_means, double scale, double beta,
+                      int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens,
+                      void* out, const int64_t* out_index, int32_t* counts,
+                      uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
+                      const void* qk_int8_tiles, const float* qk_int8_scales,
+                      int workgroup_form, void* stream,
+                       const float* chunk_sums);
+
 }  // namespace
 
 extern "C" {
@@ -224,7 +244,8 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
                  const int64_t* v_strides, const int64_t* key_index, const int32_t* key_lengths,
                  int64_t sequence_length, int64_t batch, int64_t key_tokens, int64_t heads,
                  int64_t head_dim, void* ctiles, void* tiles,
-                 float* chunk_sums, float* key_mean, float* key_var, void* stream) {
+                 float* chunk_sums, float* key_mean, float* key_var, void* stream,
+                 bool fold_in_attention = false) {
   static thread_local std::string msg;
   auto err = [&](int code, const char* what) {
     msg = std::string(who) + ": " + what;
@@ -260,6 +281,7 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
   p.NKB = int(nkb);
   p.NCT = int(cdiv(nkb, SOL_BLOCK));
   p.NCHP = p.NCT * (SOL_BLOCK / sol::kPoolChunk);
+  p.fold_in_attention = fold_in_attention ? 1 : 0;
   return hip_status(sol::launch_pool(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
@@ -402,89 +424,12 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
                       const void* qk_int8_tiles, const float* qk_int8_scales,
                       int workgroup_form, void* stream) {
-  if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
-      key_tokens >= (int64_t(1) << 30))
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: unsupported shape (head_dim must be 64 or 128)");
-  const int arc = attention_args_ok("sol_attention_fwd", q, q_strides, query_index != nullptr, batch,
-                                    query_tokens, heads, scale, beta, kv_sink_tokens, query_sink_tokens, out);
-  if (arc != SOL_OK) return arc;
-  if ((query_index || out_index) && sequence_length <= 0)
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_index / out_index need sequence_length > 0");
-  if (workgroup_form < 0 || workgroup_form > 2)
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: workgroup_form must be 0, 1 or 2");
-  if ((qk_int8_tiles == nullptr) != (qk_int8_scales == nullptr) || (qk_int8_tiles && !aligned16(qk_int8_tiles)))
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: qk_int8_tiles (16-byte aligned) and qk_int8_scales go together");
-  const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
-  // Without centroid tiles the launch pools the keys itself (or, at beta =
-  // -inf, needs none).
-  const bool self_pooled = !ctiles && force != 1;
-  if (self_pooled && (tiles || key_lengths || query_index || key_cov || qk_int8_tiles || route_workspace ||
-                      workgroup_form != 0 || !pools_keys(batch, query_tokens, key_tokens, heads, head_dim)))
-    return fail(SOL_ERR_INVALID,
-                "sol_attention_fwd: ctiles may be NULL only at beta = -inf or where sol_attention_pools_keys "
-                "holds (plain K / V rows, no key_lengths, query_index, key_cov, INT8 tiles or route_workspace, "
-                "workgroup_form 0)");
-  if ((ctiles && !aligned16(ctiles)) || (tiles && !aligned16(tiles)) ||
-      (split_workspace && !aligned16(split_workspace)) || (route_workspace && !aligned16(route_workspace)))
-    return fail(SOL_ERR_INVALID,
-                "sol_attention_fwd: tiles/ctiles/split_workspace/route_workspace must be 16-byte aligned "
-                "device buffers");
-  if (query_means && !route_workspace)
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_means are read only with a route_workspace");
-  if (!tiles) {
-    const int rc = rows_mode_ok("sol_attention_fwd", k, k_strides, v, v_strides, key_lengths, key_tokens);
-    if (rc != SOL_OK) return rc;
-  }
-  if (force == 0 && !self_pooled && (!key_mean || !key_var))
-    return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
-  const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
-  const int64_t nqb = cdiv(query_tokens, SOL_BLOCK);
-  sol::AttnParams p;
-  std::memset(&p, 0, sizeof(p));
-  p.q = rows_of(q, q_strides, query_index, query_tokens, sequence_length);
-  p.pair_stride = pair_strides;
-  p.klen = key_lengths;
-  p.out_index = out_index;
-  p.out_rows = sequence_length;
-  p.workgroup_form = workgroup_form;
-  p.k8 = static_cast<const int8_t*>(qk_int8_tiles);
-  p.k8_scale = qk_int8_scales;
-  p.tiles = static_cast<const uint16_t*>(tiles);
-  if (!tiles) {
-    p.k = rows_of(k, k_strides, nullptr, key_tokens);
-    p.v = rows_of(v, v_strides, nullptr, key_tokens);
-  }
-  p.ctiles = static_cast<const uint16_t*>(ctiles);
-  p.mean = key_mean;
-  p.var = key_var;
-  p.cov = force == 0 ? key_cov : nullptr;
-  p.protection = protection;
-  p.out = static_cast<uint16_t*>(out);
-  p.counts = counts;
-  p.dbg_selected = debug_selected;
-  p.dbg_proxy = debug_proxy;
-  p.dbg_cutoff = debug_cutoff;
-  p.B = int(batch);
-  p.H = int(heads);
-  p.Tq = int(query_tokens);
-  p.Tk = int(key_tokens);
-  p.NQB = int(nqb);
-  p.NKB = int(nkb);
-  p.NCT = int(cdiv(nkb, SOL_BLOCK));
-  p.scale = float(scale);
-  p.scale_log2 = float(scale * 1.4426950408889634);
-  p.beta = force == 0 ? float(beta) : 0.f;
-  p.force = force;
-  const int64_t big = int64_t(1) << 30;
-  p.local_blocks = int(local_blocks < 0 ? -1 : (local_blocks > big ? big : local_blocks));
-  p.kv_sink_blocks = int(cdiv(kv_sink_tokens > big ? big : kv_sink_tokens, SOL_BLOCK));
-  p.q_sink_blocks = int(sink_blocks(query_sink_tokens));
-  p.splits = split_workspace ? sink_splits(batch * heads, nqb, nkb, p.q_sink_blocks, force, head_dim) : 1;
-  p.partial = p.splits > 1 ? static_cast<float*>(split_workspace) : nullptr;
-  p.mask = force != 1 ? static_cast<uint32_t*>(route_workspace) : nullptr;
-  p.NW = int(cdiv(nkb, 32));
-  p.qc = query_means;
-  return hip_status(sol::launch_sol(p, int(head_dim), static_cast<hipStream_t>(stream)));
+  return attention_fwd_impl(q, q_strides, query_index, sequence_length, batch, query_tokens, key_tokens,
+                            key_lengths, heads, head_dim, k, k_strides, v, v_strides, tiles, ctiles, key_mean,
+                            key_var, key_cov, protection, pair_strides, split_workspace, route_workspace,
+                            query_means, scale, beta, local_blocks, kv_sink_tokens, query_sink_tokens, out,
+                            out_index, counts, debug_selected, debug_proxy, debug_cutoff, qk_int8_tiles,
+                            qk_int8_scales, workgroup_form, stream, nullptr);
 }
 
 int sol_quantize_keys(const void* k, const int64_t* k_strides, const int64_t* key_index,
@@ -573,6 +518,115 @@ int sol_dense_fwd(const void* q, const int64_t* q_strides, const int64_t* query_
 
 namespace {
 
+int attention_fwd_impl(const void* q, const int64_t* q_strides, const int64_t* query_index,
+                      int64_t sequence_length, int64_t batch, int64_t query_tokens,
+                      int64_t key_tokens,
+                      const int32_t* key_lengths, int64_t heads, int64_t head_dim,
+                      const void* k, const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                      const void* tiles, const void* ctiles, const float* key_mean,
+                      const float* key_var, const float* key_cov, const uint8_t* protection,
+                      const int32_t* pair_strides, void* split_workspace, void* route_workspace,
+                      const float* query_means, double scale, double beta,
+                      int64_t local_blocks, int64_t kv_sink_tokens, int64_t query_sink_tokens,
+                      void* out, const int64_t* out_index, int32_t* counts,
+                      uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
+                      const void* qk_int8_tiles, const float* qk_int8_scales,
+                      int workgroup_form, void* stream,
+                       const float* chunk_sums) {
+  if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
+      key_tokens >= (int64_t(1) << 30))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: unsupported shape (head_dim must be 64 or 128)");
+  const int arc = attention_args_ok("sol_attention_fwd", q, q_strides, query_index != nullptr, batch,
+                                    query_tokens, heads, scale, beta, kv_sink_tokens, query_sink_tokens, out);
+  if (arc != SOL_OK) return arc;
+  if ((query_index || out_index) && sequence_length <= 0)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_index / out_index need sequence_length > 0");
+  if (workgroup_form < 0 || workgroup_form > 2)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: workgroup_form must be 0, 1 or 2");
+  if ((qk_int8_tiles == nullptr) != (qk_int8_scales == nullptr) || (qk_int8_tiles && !aligned16(qk_int8_tiles)))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: qk_int8_tiles (16-byte aligned) and qk_int8_scales go together");
+  const int force = std::isinf(beta) ? (beta < 0 ? 1 : 2) : 0;
+  // Without centroid tiles the launch pools the keys itself (or, at beta =
+  // -inf, needs none).
+  const bool self_pooled = !ctiles && force != 1;
+  if (self_pooled && (tiles || key_lengths || query_index || key_cov || qk_int8_tiles || route_workspace ||
+                      workgroup_form != 0 || !pools_keys(batch, query_tokens, key_tokens, heads, head_dim)))
+    return fail(SOL_ERR_INVALID,
+                "sol_attention_fwd: ctiles may be NULL only at beta = -inf or where sol_attention_pools_keys "
+                "holds (plain K / V rows, no key_lengths, query_index, key_cov, INT8 tiles or route_workspace, "
+                "workgroup_form 0)");
+  if ((ctiles && !aligned16(ctiles)) || (tiles && !aligned16(tiles)) ||
+      (split_workspace && !aligned16(split_workspace)) || (route_workspace && !aligned16(route_workspace)))
+    return fail(SOL_ERR_INVALID,
+                "sol_attention_fwd: tiles/ctiles/split_workspace/route_workspace must be 16-byte aligned "
+                "device buffers");
+  if (query_means && !route_workspace)
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: query_means are read only with a route_workspace");
+  if (!tiles) {
+    const int rc = rows_mode_ok("sol_attention_fwd", k, k_strides, v, v_strides, key_lengths, key_tokens);
+    if (rc != SOL_OK) return rc;
+  }
+  if (chunk_sums && (force != 0 || self_pooled || key_lengths || route_workspace || key_cov ||
+                     !sol::folds_moments(cdiv(key_tokens, SOL_BLOCK))))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: chunk sums in place of the moments need finite beta, "
+                                 "17..255 key blocks, no key_lengths, route_workspace or key_cov");
+  if (force == 0 && !self_pooled && !chunk_sums && (!key_mean || !key_var))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
+  const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
+  const int64_t nqb = cdiv(query_tokens, SOL_BLOCK);
+  sol::AttnParams p;
+  std::memset(&p, 0, sizeof(p));
+  p.q = rows_of(q, q_strides, query_index, query_tokens, sequence_length);
+  p.pair_stride = pair_strides;
+  p.klen = key_lengths;
+  p.out_index = out_index;
+  p.out_rows = sequence_length;
+  p.workgroup_form = workgroup_form;
+  p.k8 = static_cast<const int8_t*>(qk_int8_tiles);
+  p.k8_scale = qk_int8_scales;
+  p.tiles = static_cast<const uint16_t*>(tiles);
+  if (!tiles) {
+    p.k = rows_of(k, k_strides, nullptr, key_tokens);
+    p.v = rows_of(v, v_strides, nullptr, key_tokens);
+  }
+  p.ctiles = static_cast<const uint16_t*>(ctiles);
+  p.mean = chunk_sums ? nullptr : key_mean;
+  p.var = chunk_sums ? nullptr : key_var;
+  p.ksum = chunk_sums;
+  p.cov = force == 0 ? key_cov : nullptr;
+  p.protection = protection;
+  p.out = static_cast<uint16_t*>(out);
+  p.counts = counts;
+  p.dbg_selected = debug_selected;
+  p.dbg_proxy = debug_proxy;
+  p.dbg_cutoff = debug_cutoff;
+  p.B = int(batch);
+  p.H = int(heads);
+  p.Tq = int(query_tokens);
+  p.Tk = int(key_tokens);
+  p.NQB = int(nqb);
+  p.NKB = int(nkb);
+  p.NCT = int(cdiv(nkb, SOL_BLOCK));
+  p.scale = float(scale);
+  p.scale_log2 = float(scale * 1.4426950408889634);
+  p.beta = force == 0 ? float(beta) : 0.f;
+  p.force = force;
+  const int64_t big = int64_t(1) << 30;
+  p.local_blocks = int(local_blocks < 0 ? -1 : (local_blocks > big ? big : local_blocks));
+  p.kv_sink_blocks = int(cdiv(kv_sink_tokens > big ? big : kv_sink_tokens, SOL_BLOCK));
+  p.q_sink_blocks = int(sink_blocks(query_sink_tokens));
+  p.splits = split_workspace ? sink_splits(batch * heads, nqb, nkb, p.q_sink_blocks, force, head_dim) : 1;
+  p.partial = p.splits > 1 ? static_cast<float*>(split_workspace) : nullptr;
+  p.mask = force != 1 ? static_cast<uint32_t*>(route_workspace) : nullptr;
+  p.NW = int(cdiv(nkb, 32));
+  p.qc = query_means;
+  return hip_status(sol::launch_sol(p, int(head_dim), static_cast<hipStream_t>(stream)));
+}
+
+// Query-block pairs (over all entries and heads) up to which an all-in launch
+// folds the key moments inside the attention kernel (all_in).
+constexpr int64_t kFoldMaxPairs = 512;
+
 // Byte layout of the all-in workspace: the sol_pool_kv buffers, 256-byte
 // aligned, in the order sol_pool_sizes lists them (the block tiles only
 // outside rows mode, the moment buffers only at finite beta), then the split
@@ -651,14 +705,24 @@ int all_in(const char* who, const void* q, const int64_t* q_strides, const void*
   float* mean = l.moments ? reinterpret_cast<float*>(ws + l.mean) : nullptr;
   float* var = l.moments ? reinterpret_cast<float*>(ws + l.var) : nullptr;
   void* tiles = rows ? nullptr : ws + l.tiles;
+  // Moments of 17..255 key blocks in a launch of at most one round of
+  // workgroups: the attention workgroups fold the chunk sums themselves (the
+  // same bits) and the moments_kernel launch, latency on that short
+  // critical path, goes.  Longer launches keep it: there every workgroup's
+  // fold (loads before its cutoff) costs more than one launch.  All-in
+  // calls, one box, alternating libraries, us: 4,096 tokens x 4 heads 44.3 ->
+  // 43.4, 8,192 x 4 70.9 -> 70.1, 4,096 x 16 73.5 -> 71.3; 2 x 4,096 x 16
+  // (1,024 two-block workgroups) 163.7 -> 165.2.
+  const bool fold = l.moments && sol::folds_moments(cdiv(key_tokens, SOL_BLOCK)) &&
+                    batch * heads * cdiv(cdiv(query_tokens, SOL_BLOCK), 2) <= kFoldMaxPairs;
   const int prc = pool_checked(who, k, k_strides, v, v_strides, nullptr, nullptr, 0, batch, key_tokens, heads,
-                               head_dim, ws, tiles, sums, mean, var, stream);
+                               head_dim, ws, tiles, sums, mean, var, stream, fold);
   if (prc != SOL_OK) return prc;
-  return sol_attention_fwd(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
-                           head_dim, k, k_strides, v, v_strides, tiles, ws, mean, var, nullptr, nullptr, nullptr,
-                           l.split_bytes ? ws + l.split : nullptr, nullptr /* routing in the attention kernel */,
-                           nullptr, scale, beta, local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr,
-                           counts, nullptr, nullptr, nullptr, nullptr, nullptr, 0, stream);
+  return attention_fwd_impl(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
+                            head_dim, k, k_strides, v, v_strides, tiles, ws, mean, var, nullptr, nullptr, nullptr,
+                            l.split_bytes ? ws + l.split : nullptr, nullptr /* routing in the attention kernel */,
+                            nullptr, scale, beta, local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr,
+                            counts, nullptr, nullptr, nullptr, nullptr, nullptr, 0, stream, fold ? sums : nullptr);
 }
 
 }  // namespace

@@ -412,8 +412,9 @@ hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
       hipLaunchKernelGGL((pool_kv_kernel<64, 4>), grid, dim3(256), 0, stream, p);
   }
   hipError_t err = hipGetLastError();
-  // Single-chunk keys had their moments written by the pooling kernel.
-  if (err != hipSuccess || !p.ksum || !p.ctiles || p.NKB <= kPoolChunk) return err;
+  // Single-chunk keys had their moments written by the pooling kernel; with
+  // fold_in_attention the attention launch folds the chunk sums itself.
+  if (err != hipSuccess || !p.ksum || !p.ctiles || p.NKB <= kPoolChunk || p.fold_in_attention) return err;
   if (D == 128)
     hipLaunchKernelGGL(moments_kernel<128>, dim3(p.B * p.H), dim3(kMomentThreads), 0, stream,
                        p.ksum, p.mean, p.var, p.klen, p.Tk, p.NKB, p.H);

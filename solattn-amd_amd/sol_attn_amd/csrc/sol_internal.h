@@ -26,7 +26,16 @@ struct PoolParams {
   float* var;        // [B, H, D]
   int B, H, Tk, NKB, NCT, NCHP;  // NCHP = 4 * NCT pooling chunks of 16 blocks
                                  // (NKB, NCT: for Tk; ragged entries use a prefix)
+  int fold_in_attention;  // 1: no moments_kernel launch; the attention launch folds
+                          // the chunk sums itself (AttnParams::ksum, folds_moments)
 };
+
+// Key sequences whose moments the attention kernels fold from the pooling
+// pass's chunk sums (AttnParams::ksum) instead of a moments_kernel launch:
+// more than one 16-block chunk (one chunk's moments the pooling kernel writes
+// itself) and fewer than 16 whole chunks, where moments_kernel's cascade is a
+// plain sequential fold that one thread per feature repeats in a few adds.
+inline bool folds_moments(int64_t nkb) { return nkb > kPoolChunk && nkb < 16 * kPoolChunk; }
 
 // Full key covariance (covariance.hip): the full-covariance threshold
 // experiment.  Partial sums over kCovSplit centroid ranges per (entry, head).
@@ -65,6 +74,8 @@ struct AttnParams {
   const uint16_t* ctiles;      // [B, H, NCT, 2, 64 * D] centroid tiles
   const float* mean;           // [B, H, D]
   const float* var;            // [B, H, D]
+  const float* ksum;           // [B, H, NCH, 2, D] pooling chunk sums, or null: when set (mean / var
+                               // null, folds_moments(NKB), no klen) the cutoff stage folds the moments
   const float* cov;            // [B, H, D, D] full key covariance, or null: diagonal (var)
   const int8_t* k8;            // [B, H, NKB, 64 * D] INT8 K tiles (quantised-QK experiment), or null
   const float* k8_scale;       // [B, H, NKB] their scales

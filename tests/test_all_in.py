@@ -7,10 +7,12 @@ aligned otherwise, the block tiles only outside rows mode, no moments at
 beta = +inf, the split workspace) and its rejections; argument errors of the
 entry point before any launch.
 GPU: outputs and counts bit-identical to sol_pool_kv + sol_attention_fwd
-(the same kernels and workspace layout) on every path the call can take --
-keys pooled inside the launch, the small-launch kernel after the pooling
-kernel, split query sinks, the one-block kernel, block tiles for fewer than
-64 keys, beta = +inf, head-strided K / V -- and against the oracle on one case.
+(the same kernels and workspace layout, the moments from moments_kernel) on
+every path the call can take -- keys pooled inside the launch, the
+small-launch kernel after the pooling kernel, split query sinks, the
+one-block kernel, block tiles for fewer than 64 keys, beta = +inf,
+head-strided K / V, key moments folded inside the attention launch from 2 to
+16 chunk sums -- and against the oracle on one case.
 """
 
 import ctypes
@@ -98,7 +100,9 @@ CASES = [(1, 1024, 1024, 8, 64, 1.0, 128, 128, "smooth"),    # keys pooled insid
          (2, 4096, 4096, 16, 128, 0.5, 64, 0, "random"),     # two-block workgroups, moments fold
          (1, 300, 40, 2, 64, 1.0, 0, 0, "random"),           # fewer keys than a block: block tiles
          (2, 700, 1000, 3, 128, math.inf, 64, 64, "random"),  # beta = +inf: no moments
-         (1, 2000, 1500, 2, 64, 1.0, 0, 64, "strided")]      # head-strided K / V views
+         (1, 2000, 1500, 2, 64, 1.0, 0, 64, "strided"),     # head-strided K / V views, moments folded
+         (1, 1024, 2000, 4, 128, 1.0, 64, 0, "random"),     # small-launch kernel folding 2 chunks
+         (1, 512, 16000, 2, 64, 0.5, 0, 64, "random")]      # 250 key blocks: 15 whole chunks + a partial
 
 
 def _inputs(case):
