@@ -195,7 +195,8 @@ __device__ __forceinline__ void centroid_tile(State<D>& st, const uint16_t* buf,
 // cores (D / 32 products per 32-key half instead of D / 16), then the INT32
 // scores converted to FP32 and scaled inside the softmax by c8 = c s_q s_k
 // (the lane's query scale, the tile's key scale); absent keys of the tail
-// block (TAIL) start at -inf.  The softmax and O^T += V^T P^T are those of
+// block (TAIL) start at -inf.  The softmax (FastHalf, which re-forms a
+// half's integer scores in the uncommon case) and O^T += V^T P^T are those of
 // tile_attend, with the same in-wave interleave: half 0's products; half
 // 1's products with half 0's softmax and V^T reads; half 0's P V with half
 // 1's softmax; half 1's P V.  The refill's DMA rounds are spread over the
@@ -226,7 +227,16 @@ __device__ __forceinline__ void tile_attend_i8(State<D>& st, const uint16_t* buf
   i32x4 k0[K8], k1[K8];
 #pragma unroll
   for (int ks = 0; ks < K8; ++ks) k0[ks] = kfrag(0, ks);
-  HalfSoftmax<D> h0, h1;
+  // The scores of half t again (FastHalf::resolve), from the tile still in LDS.
+  auto raw = [&](int t) {
+    i32x16 x;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) x[e] = 0;
+#pragma unroll
+    for (int ks = 0; ks < K8; ++ks) x = mfma32x32x32i8(kfrag(t, ks), q8[ks], x);
+    return to_scores(x, t);
+  };
+  FastHalf<D> h0, h1;
   i32x16 i0, i1;
 #pragma unroll
   for (int e = 0; e < 16; ++e) i0[e] = i1[e] = 0;
@@ -249,7 +259,7 @@ __device__ __forceinline__ void tile_attend_i8(State<D>& st, const uint16_t* buf
     refill.template after_step<2 * K8>(K8 + ks);
     chunk_end();
   }
-  if (h0.rescale) rescale_acc<D>(st, h0.alpha);
+  h0.resolve(st, c8, [&] { return raw(0); });
   u32x4 vb[2][DT];
 #pragma unroll
   for (int f = 0; f < 2 * DT; ++f) {
@@ -260,7 +270,7 @@ __device__ __forceinline__ void tile_attend_i8(State<D>& st, const uint16_t* buf
     h1.template part<2 * DT>(f, st, c8);
     chunk_end();
   }
-  if (h1.rescale) rescale_acc<D>(st, h1.alpha);
+  h1.resolve(st, c8, [&] { return raw(1); });
 #pragma unroll
   for (int f = 0; f < 2 * DT; ++f) {
     const int c4 = f / DT, dt = f % DT;
