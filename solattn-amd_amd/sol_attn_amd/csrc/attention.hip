@@ -497,41 +497,81 @@ __device__ __forceinline__ float query_mean(const uint16_t* rows, int qlen, int 
   return __fdiv_rn(tot, float(qlen));
 }
 
-// Key moments of feature f of head `head` (kernels.py:30-49: mean and
-// clamped population variance of the BF16 centroids) folded from the
-// pooling pass's chunk sums (AttnParams::ksum) for folds_moments key
-// sequences, in moments_kernel's order: the whole 16-block chunks summed in
-// turn from 0, the partial chunk's sum (or 0) added to that, then the two
-// 256-block levels (0 below 256 blocks), and the divisions by NKB.  The same
-// roundings in the same order as moments_kernel, so the same bits.
+// Key moments (kernels.py:30-49: mean and clamped population variance of
+// the BF16 centroids) of one feature of one head for the cutoff stage, loaded
+// before the query mean (load) and formed after it (finish), so the loads'
+// latency hides behind the query mean.  Three sources:
+// - the pooling pass's mean and variance (AttnParams::mean / var);
+// - its chunk sums (AttnParams::ksum, folds_moments key sequences), folded
+//   in moments_kernel's order: the whole 16-block chunks summed in turn from
+//   0, the partial chunk's sum (or 0) added to that, then the two 256-block
+//   levels (0 below 256 blocks), and the divisions by NKB;
+// - the K centroids of centroid tile 0 (AttnParams::tile_moments, at most 16
+//   key blocks), with the pooling kernel's one-chunk formula: the centroids
+//   summed in turn from 0, their squares likewise, the divisions by NKB.
+// Either way the same roundings in the same order as the pooling kernels,
+// so the same bits.  Every load is unconditional (indices clamped into the
+// buffers) so that they issue back to back.
 template <int D>
-__device__ __forceinline__ void fold_moments(const AttnParams& p, int64_t head, int f, float& mu, float& var) {
-  const int nch = (p.NKB + kPoolChunk - 1) / kPoolChunk;
-  const int full = p.NKB / kPoolChunk;  // <= 15
-  const bool partial = full * kPoolChunk < p.NKB;
-  const float* base = p.ksum + head * nch * 2 * D + f;
-  float x[2][16];
+struct KeyMoments {
+  float x[2][16];  // chunk sums and sums of squares, or the centroids (x[0])
+  float mu = 0.f, var = 0.f;
+
+  __device__ __forceinline__ void load(const AttnParams& p, int64_t head, int f) {
+    using TL = TileLayout<D>;
+    if (p.ksum) {
+      const int nch = (p.NKB + kPoolChunk - 1) / kPoolChunk;  // <= 16
+      const float* base = p.ksum + head * nch * 2 * D + f;
 #pragma unroll
-  for (int c = 0; c < 16; ++c) {  // all loads first
-    const bool take = c < full || (c == full && partial);
-    x[0][c] = take ? base[(2 * c) * D] : 0.f;
-    x[1][c] = take ? base[(2 * c + 1) * D] : 0.f;
-  }
-  float a[2] = {0.f, 0.f}, r[2] = {0.f, 0.f};
+      for (int c = 0; c < 16; ++c) {
+        const int cc = min(c, nch - 1);
+        x[0][c] = base[(2 * cc) * D];
+        x[1][c] = base[(2 * cc + 1) * D];
+      }
+    } else if (p.tile_moments) {
+      const uint16_t* kt = p.ctiles + head * p.NCT * 2 * TL::kElems;  // tile 0, its K half
 #pragma unroll
-  for (int c = 0; c < 16; ++c)
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      if (c < full) a[w] = __fadd_rn(a[w], x[w][c]);
-      else if (c == full && partial) r[w] = x[w][c];
+      for (int r = 0; r < 16; ++r) x[0][r] = bf16_bits_to_f32(kt[TL::k_offset(r, f / 8) + f % 8]);
+    } else {
+      mu = p.mean[head * D + f];
+      var = p.cov ? 0.f : p.var[head * D + f];
     }
-  const float n = float(p.NKB);
-  const float m = __fdiv_rn(__fadd_rn(__fadd_rn(__fadd_rn(r[0], a[0]), 0.f), 0.f), n);
-  const float sq = __fdiv_rn(__fadd_rn(__fadd_rn(__fadd_rn(r[1], a[1]), 0.f), 0.f), n);
-  const float v = __fsub_rn(sq, __fmul_rn(m, m));
-  mu = m;
-  var = v > 0.f ? v : 0.f;
-}
+  }
+
+  __device__ __forceinline__ void finish(const AttnParams& p) {
+    const float n = float(p.NKB);
+    if (p.ksum) {
+      const int full = p.NKB / kPoolChunk;  // <= 15
+      const bool partial = full * kPoolChunk < p.NKB;
+      float a[2] = {0.f, 0.f}, r[2] = {0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 16; ++c)
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          if (c < full) a[w] = __fadd_rn(a[w], x[w][c]);
+          else if (c == full && partial) r[w] = x[w][c];
+        }
+      const float m = __fdiv_rn(__fadd_rn(__fadd_rn(__fadd_rn(r[0], a[0]), 0.f), 0.f), n);
+      const float sq = __fdiv_rn(__fadd_rn(__fadd_rn(__fadd_rn(r[1], a[1]), 0.f), 0.f), n);
+      const float v = __fsub_rn(sq, __fmul_rn(m, m));
+      mu = m;
+      var = v > 0.f ? v : 0.f;
+    } else if (p.tile_moments) {
+      float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        if (r < p.NKB) {
+          s1 = __fadd_rn(s1, x[0][r]);
+          s2 = __fadd_rn(s2, __fmul_rn(x[0][r], x[0][r]));
+        }
+      }
+      const float m = __fdiv_rn(s1, n);
+      const float v = __fsub_rn(__fdiv_rn(s2, n), __fmul_rn(m, m));
+      mu = m;
+      var = v > 0.f ? v : 0.f;
+    }
+  }
+};
 
 // The cutoff from the workgroup-summed terms: sum Qc mu + beta sqrt(the
 // quadratic form), which the full covariance may round below 0
@@ -687,21 +727,15 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   const bool routed = p.mask != nullptr;  // decisions precomputed by route_kernel
   if (p.force == 0 && !routed) {
     const int qlen = live ? min(kBlock, p.Tq - qb * kBlock) : 1;
-    float mu = 0.f, vr = 0.f;  // this thread's feature of the key moments, loads issued first
-    if (lt < D) {
-      if (p.ksum) {
-        fold_moments<D>(p, head, lt, mu, vr);
-      } else {
-        mu = p.mean[head * D + lt];
-        vr = p.cov ? 0.f : p.var[head * D + lt];
-      }
-    }
+    KeyMoments<D> km;  // this thread's feature of the key moments, loads issued first
+    if (lt < D) km.load(p, head, lt);
     if (lt < D) s_qm[qg][lt] = query_mean<D>(ring + qg * kBlock * S::KS, qlen, lt);
     __syncthreads();
     float a = 0.f, g = 0.f;
     if (lt < D) {
+      km.finish(p);
       const float qm = s_qm[qg][lt];
-      a = qm * mu;
+      a = qm * km.mu;
       if (p.cov) {
         // Full covariance: this feature's term of Qc^T cov Qc.  cov is
         // symmetric bit for bit, so thread lt reads column lt (coalesced).
@@ -710,7 +744,7 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
         for (int e = 0; e < D; ++e) sq = fmaf(col[e * D], s_qm[qg][e], sq);
         g = qm * sq;
       } else {
-        g = qm * qm * vr;
+        g = qm * qm * km.var;
       }
     }
 #pragma unroll
@@ -1115,21 +1149,20 @@ __global__ __launch_bounds__(128 * KS, KS / 2) void sol_small_kernel(AttnParams 
   // thread forms the cutoff from the published sums).
   float cut = 0.f;
   if (p.force == 0 && !routed) {
-    float mu = 0.f, vr = 0.f;  // this thread's feature of the key moments (pooled here: below)
-    if (!POOL && tid < D) {
-      if (p.ksum) {
-        fold_moments<D>(p, head, tid, mu, vr);
-      } else {
-        mu = p.mean[head * D + tid];
-        vr = p.cov ? 0.f : p.var[head * D + tid];
-      }
-    }
+    KeyMoments<D> km;  // this thread's feature of the key moments (pooled here: below)
+    if (!POOL && tid < D) km.load(p, head, tid);
     if (tid < D) s_qm[tid] = query_mean<D>(ring, qlen, tid);
     __syncthreads();  // also: every read of the Q staging rows is done
     float a = 0.f, g = 0.f;
     if (tid < D) {
       const float qm = s_qm[tid];
-      if (POOL) mu = s_mom[0][tid];
+      float mu;
+      if (POOL) {
+        mu = s_mom[0][tid];
+      } else {
+        km.finish(p);
+        mu = km.mu;
+      }
       a = qm * mu;
       if (p.cov) {
         const float* col = p.cov + int64_t(head) * D * D + tid;  // symmetric: column tid
@@ -1137,7 +1170,7 @@ __global__ __launch_bounds__(128 * KS, KS / 2) void sol_small_kernel(AttnParams 
         for (int e = 0; e < D; ++e) sq = fmaf(col[e * D], s_qm[e], sq);
         g = qm * sq;
       } else {
-        g = qm * qm * (POOL ? s_mom[1][tid] : vr);
+        g = qm * qm * (POOL ? s_mom[1][tid] : km.var);
       }
     }
 #pragma unroll

@@ -214,7 +214,7 @@ int attention_fwd_impl(const void* q, const int64_t* q_strides, const int64_t* q
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
                       const void* qk_int8_tiles, const float* qk_int8_scales,
                       int workgroup_form, void* stream,
-                       const float* chunk_sums);
+                       const float* chunk_sums, bool tile_moments);
 
 }  // namespace
 
@@ -245,7 +245,7 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
                  int64_t sequence_length, int64_t batch, int64_t key_tokens, int64_t heads,
                  int64_t head_dim, void* ctiles, void* tiles,
                  float* chunk_sums, float* key_mean, float* key_var, void* stream,
-                 bool fold_in_attention = false) {
+                 bool fold_in_attention = false, bool blocks_only = false) {
   static thread_local std::string msg;
   auto err = [&](int code, const char* what) {
     msg = std::string(who) + ": " + what;
@@ -282,6 +282,10 @@ int pool_checked(const char* who, const void* k, const int64_t* k_strides, const
   p.NCT = int(cdiv(nkb, SOL_BLOCK));
   p.NCHP = p.NCT * (SOL_BLOCK / sol::kPoolChunk);
   p.fold_in_attention = fold_in_attention ? 1 : 0;
+  // Centroid tiles only (all_in): plain rows, at most 16 blocks, nothing else.
+  if (blocks_only && (tiles || !ctiles || key_index || key_lengths || moments || nkb > sol::kPoolChunk))
+    return err(SOL_ERR_INVALID, "centroid-only pooling needs plain rows, ctiles only and at most 16 key blocks");
+  p.blocks_only = blocks_only ? 1 : 0;
   return hip_status(sol::launch_pool(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
@@ -429,7 +433,7 @@ int sol_attention_fwd(const void* q, const int64_t* q_strides, const int64_t* qu
                             key_var, key_cov, protection, pair_strides, split_workspace, route_workspace,
                             query_means, scale, beta, local_blocks, kv_sink_tokens, query_sink_tokens, out,
                             out_index, counts, debug_selected, debug_proxy, debug_cutoff, qk_int8_tiles,
-                            qk_int8_scales, workgroup_form, stream, nullptr);
+                            qk_int8_scales, workgroup_form, stream, nullptr, false);
 }
 
 int sol_quantize_keys(const void* k, const int64_t* k_strides, const int64_t* key_index,
@@ -532,7 +536,7 @@ int attention_fwd_impl(const void* q, const int64_t* q_strides, const int64_t* q
                       uint8_t* debug_selected, float* debug_proxy, float* debug_cutoff,
                       const void* qk_int8_tiles, const float* qk_int8_scales,
                       int workgroup_form, void* stream,
-                       const float* chunk_sums) {
+                       const float* chunk_sums, bool tile_moments) {
   if (!shape_ok(batch, query_tokens, heads, head_dim) || key_tokens <= 0 ||
       key_tokens >= (int64_t(1) << 30))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: unsupported shape (head_dim must be 64 or 128)");
@@ -570,7 +574,11 @@ int attention_fwd_impl(const void* q, const int64_t* q_strides, const int64_t* q
                      !sol::folds_moments(cdiv(key_tokens, SOL_BLOCK))))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: chunk sums in place of the moments need finite beta, "
                                  "17..255 key blocks, no key_lengths, route_workspace or key_cov");
-  if (force == 0 && !self_pooled && !chunk_sums && (!key_mean || !key_var))
+  if (tile_moments && (force != 0 || self_pooled || chunk_sums || key_lengths || route_workspace || key_cov ||
+                       !ctiles || cdiv(key_tokens, SOL_BLOCK) > sol::kPoolChunk))
+    return fail(SOL_ERR_INVALID, "sol_attention_fwd: moments from the centroid tile need finite beta, "
+                                 "ctiles, at most 16 key blocks, no key_lengths, route_workspace or key_cov");
+  if (force == 0 && !self_pooled && !chunk_sums && !tile_moments && (!key_mean || !key_var))
     return fail(SOL_ERR_INVALID, "sol_attention_fwd: finite beta needs key_mean and key_var");
   const int64_t nkb = cdiv(key_tokens, SOL_BLOCK);
   const int64_t nqb = cdiv(query_tokens, SOL_BLOCK);
@@ -590,9 +598,10 @@ int attention_fwd_impl(const void* q, const int64_t* q_strides, const int64_t* q
     p.v = rows_of(v, v_strides, nullptr, key_tokens);
   }
   p.ctiles = static_cast<const uint16_t*>(ctiles);
-  p.mean = chunk_sums ? nullptr : key_mean;
-  p.var = chunk_sums ? nullptr : key_var;
+  p.mean = chunk_sums || tile_moments ? nullptr : key_mean;
+  p.var = chunk_sums || tile_moments ? nullptr : key_var;
   p.ksum = chunk_sums;
+  p.tile_moments = tile_moments ? 1 : 0;
   p.cov = force == 0 ? key_cov : nullptr;
   p.protection = protection;
   p.out = static_cast<uint16_t*>(out);
@@ -715,14 +724,22 @@ int all_in(const char* who, const void* q, const int64_t* q_strides, const void*
   // (1,024 two-block workgroups) 163.7 -> 165.2.
   const bool fold = l.moments && sol::folds_moments(cdiv(key_tokens, SOL_BLOCK)) &&
                     batch * heads * cdiv(cdiv(query_tokens, SOL_BLOCK), 2) <= kFoldMaxPairs;
-  const int prc = pool_checked(who, k, k_strides, v, v_strides, nullptr, nullptr, 0, batch, key_tokens, heads,
-                               head_dim, ws, tiles, sums, mean, var, stream, fold);
+  // Keys of at most one 16-block chunk in rows mode: the centroid tiles alone
+  // (pool_blocks_kernel, 16 workgroups per head instead of one per head and
+  // K / V), and the attention launch forms the moments from tile 0.
+  const bool blocks = rows && cdiv(key_tokens, SOL_BLOCK) <= sol::kPoolChunk;
+  const bool tile_moments = blocks && l.moments;
+  const int prc = blocks ? pool_checked(who, k, k_strides, v, v_strides, nullptr, nullptr, 0, batch, key_tokens,
+                                        heads, head_dim, ws, nullptr, nullptr, nullptr, nullptr, stream, false, true)
+                         : pool_checked(who, k, k_strides, v, v_strides, nullptr, nullptr, 0, batch, key_tokens,
+                                        heads, head_dim, ws, tiles, sums, mean, var, stream, fold);
   if (prc != SOL_OK) return prc;
   return attention_fwd_impl(q, q_strides, nullptr, 0, batch, query_tokens, key_tokens, nullptr, heads,
                             head_dim, k, k_strides, v, v_strides, tiles, ws, mean, var, nullptr, nullptr, nullptr,
                             l.split_bytes ? ws + l.split : nullptr, nullptr /* routing in the attention kernel */,
                             nullptr, scale, beta, local_blocks, kv_sink_tokens, query_sink_tokens, out, nullptr,
-                            counts, nullptr, nullptr, nullptr, nullptr, nullptr, 0, stream, fold ? sums : nullptr);
+                            counts, nullptr, nullptr, nullptr, nullptr, nullptr, 0, stream, fold ? sums : nullptr,
+                            tile_moments);
 }
 
 }  // namespace

@@ -170,6 +170,78 @@ void pool_kv_kernel(PoolParams p) {
   }
 }
 
+// Block centroids only, for keys of at most one 16-block chunk whose
+// attention launch forms the key moments itself from the centroid tile
+// (PoolParams::blocks_only: no chunk sums, no moments, no block tiles, plain
+// K / V rows): four waves per workgroup, each pooling one block (D = 128) or
+// two (D = 64) as pool_kv_kernel's waves do -- the same loads, the same
+// sequential 16-row sums folded in order, the same divisions, so the same
+// centroids -- and storing its centroid row straight into the tile, with no
+// LDS stage or barrier.  Every row of the tiles is written (zero past the
+// last block).  Short launches are latency-bound: the wide form's one
+// workgroup of 16 waves per (entry, head, K / V) reads the whole chunk on one
+// CU; here 16 workgroups per (entry, head) share it.
+template <int D>
+__global__ __launch_bounds__(256) void pool_blocks_kernel(PoolParams p) {
+  constexpr int DC = D / 8;          // 16-byte chunks per token row
+  constexpr int LPB = DC * 4;        // lanes per key block: 4 chunks of 16 rows
+  constexpr int BPW = kWave / LPB;   // key blocks per wave
+  constexpr int BPG = 4 * BPW;       // key blocks per workgroup
+  using TL = TileLayout<D>;
+  const bool is_v = blockIdx.y != 0;
+  const TokenRows src = is_v ? p.v : p.k;
+  const int per_head = p.NCT * kBlock / BPG;
+  const int bh = blockIdx.x / per_head, part = blockIdx.x % per_head;
+  const int h = bh % p.H, b = bh / p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int sub = lane / LPB, r4 = (lane % LPB) / DC, dc = lane % DC;
+  const int j = part * BPG + wave * BPW + sub;  // key block, < NCT * 64
+  const int nkb = (p.Tk + kBlock - 1) / kBlock;
+  float s[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s[e] = 0.f;
+  int len = 0;
+  if (j < nkb) {
+    len = min(kBlock, p.Tk - kBlock * j);
+    u32x4 x[16];
+    load_rows16<16, true>(src, b, kBlock * j + 16 * r4, kBlock * j + len - 1, h, 8 * dc, x);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (16 * r4 + i < len) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t w = x[i][e >> 1];
+          s[e] = __fadd_rn(s[e], bf16_bits_to_f32((e & 1) ? (w >> 16) : (w & 0xFFFFu)));
+        }
+      }
+    }
+  }
+  float t1[8], t2[8], t3[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    t1[e] = __shfl(s[e], lane + DC);
+    t2[e] = __shfl(s[e], lane + 2 * DC);
+    t3[e] = __shfl(s[e], lane + 3 * DC);
+  }
+  if (r4 == 0) {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float m0 = 0.f, m1 = 0.f;
+      if (len > 0) {
+        const float a0 = __fadd_rn(__fadd_rn(__fadd_rn(s[e], t1[e]), t2[e]), t3[e]);
+        const float a1 = __fadd_rn(__fadd_rn(__fadd_rn(s[e + 1], t1[e + 1]), t2[e + 1]), t3[e + 1]);
+        m0 = __fdiv_rn(a0, float(len));
+        m1 = __fdiv_rn(a1, float(len));
+      }
+      o[e >> 1] = pack_bf16x2(m0, m1);
+    }
+    uint16_t* ctile = p.ctiles + ((int64_t(b) * p.H + h) * p.NCT + j / kBlock) * 2 * TL::kElems;
+    const int row = j % kBlock;
+    *reinterpret_cast<u32x4*>(ctile + (is_v ? TL::kElems + TL::v_offset(row, dc) : TL::k_offset(row, dc))) = o;
+  }
+}
+
 // Four heads per workgroup (D = 128, heads a multiple of 4, large grids):
 // one 16-block chunk of heads h0 .. h0 + 3, sixteen waves, wave w pooling
 // key block w of the chunk.  Lane (hq, dc) reads head h0 + hq's 16-byte
@@ -399,6 +471,14 @@ constexpr int64_t kWidePoolGroups = 512;
 bool POOL_FOUR_HEADS = true;
 
 hipError_t launch_pool(const PoolParams& p, int D, hipStream_t stream) {
+  if (p.blocks_only) {
+    const unsigned per_head = unsigned(p.NCT) * kBlock / (D == 128 ? 4 : 8);
+    if (D == 128)
+      hipLaunchKernelGGL(pool_blocks_kernel<128>, dim3(unsigned(p.B) * p.H * per_head, 2), dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL(pool_blocks_kernel<64>, dim3(unsigned(p.B) * p.H * per_head, 2), dim3(256), 0, stream, p);
+    return hipGetLastError();
+  }
   const dim3 grid(unsigned(p.B) * p.H * p.NCHP, 2);
   const bool wide = 2 * int64_t(p.B) * p.H * p.NCHP <= kWidePoolGroups;
   if (D == 128 && !wide && p.H % 4 == 0 && POOL_FOUR_HEADS) {

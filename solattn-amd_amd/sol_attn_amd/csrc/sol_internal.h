@@ -28,6 +28,9 @@ struct PoolParams {
                                  // (NKB, NCT: for Tk; ragged entries use a prefix)
   int fold_in_attention;  // 1: no moments_kernel launch; the attention launch folds
                           // the chunk sums itself (AttnParams::ksum, folds_moments)
+  int blocks_only;        // 1: centroid tiles only (pool_blocks_kernel; at most 16 key
+                          // blocks, plain rows, no klen / tiles / ksum): the attention
+                          // launch forms the moments from the tile (AttnParams::tile_moments)
 };
 
 // Key sequences whose moments the attention kernels fold from the pooling
@@ -76,6 +79,8 @@ struct AttnParams {
   const float* var;            // [B, H, D]
   const float* ksum;           // [B, H, NCH, 2, D] pooling chunk sums, or null: when set (mean / var
                                // null, folds_moments(NKB), no klen) the cutoff stage folds the moments
+  int tile_moments;            // 1: mean / var null, NKB <= 16, no klen: the cutoff stage forms the
+                               // moments from the K centroids of centroid tile 0
   const float* cov;            // [B, H, D, D] full key covariance, or null: diagonal (var)
   const int8_t* k8;            // [B, H, NKB, 64 * D] INT8 K tiles (quantised-QK experiment), or null
   const float* k8_scale;       // [B, H, NKB] their scales

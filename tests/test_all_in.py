@@ -12,7 +12,9 @@ every path the call can take -- keys pooled inside the launch, the
 small-launch kernel after the pooling kernel, split query sinks, the
 one-block kernel, block tiles for fewer than 64 keys, beta = +inf,
 head-strided K / V, key moments folded inside the attention launch from 2 to
-16 chunk sums -- and against the oracle on one case.
+16 chunk sums, centroid tiles pooled alone (at most 16 key blocks) with the
+moments formed from them in the attention launch -- and against the oracle
+on one case.
 """
 
 import ctypes
@@ -102,7 +104,9 @@ CASES = [(1, 1024, 1024, 8, 64, 1.0, 128, 128, "smooth"),    # keys pooled insid
          (2, 700, 1000, 3, 128, math.inf, 64, 64, "random"),  # beta = +inf: no moments
          (1, 2000, 1500, 2, 64, 1.0, 0, 64, "strided"),     # head-strided K / V views, moments folded
          (1, 1024, 2000, 4, 128, 1.0, 64, 0, "random"),     # small-launch kernel folding 2 chunks
-         (1, 512, 16000, 2, 64, 0.5, 0, 64, "random")]      # 250 key blocks: 15 whole chunks + a partial
+         (1, 512, 16000, 2, 64, 0.5, 0, 64, "random"),      # 250 key blocks: 15 whole chunks + a partial
+         (1, 4096, 1000, 8, 64, 1.0, 64, 64, "random"),     # centroid tiles only, moments from tile 0 (D 64)
+         (2, 4096, 900, 8, 128, 0.0, 0, 128, "smooth")]     # the same in two-block workgroups (D 128)
 
 
 def _inputs(case):
