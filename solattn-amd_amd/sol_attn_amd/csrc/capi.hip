@@ -632,10 +632,6 @@ int attention_fwd_impl(const void* q, const int64_t* q_strides, const int64_t* q
   return hip_status(sol::launch_sol(p, int(head_dim), static_cast<hipStream_t>(stream)));
 }
 
-// Query-block pairs (over all entries and heads) up to which an all-in launch
-// folds the key moments inside the attention kernel (all_in).
-constexpr int64_t kFoldMaxPairs = 512;
-
 // Byte layout of the all-in workspace: the sol_pool_kv buffers, 256-byte
 // aligned, in the order sol_pool_sizes lists them (the block tiles only
 // outside rows mode, the moment buffers only at finite beta), then the split
@@ -714,16 +710,13 @@ int all_in(const char* who, const void* q, const int64_t* q_strides, const void*
   float* mean = l.moments ? reinterpret_cast<float*>(ws + l.mean) : nullptr;
   float* var = l.moments ? reinterpret_cast<float*>(ws + l.var) : nullptr;
   void* tiles = rows ? nullptr : ws + l.tiles;
-  // Moments of 17..255 key blocks in a launch of at most one round of
-  // workgroups: the attention workgroups fold the chunk sums themselves (the
-  // same bits) and the moments_kernel launch, latency on that short
-  // critical path, goes.  Longer launches keep it: there every workgroup's
-  // fold (loads before its cutoff) costs more than one launch.  All-in
-  // calls, one box, alternating libraries, us: 4,096 tokens x 4 heads 44.3 ->
-  // 43.4, 8,192 x 4 70.9 -> 70.1, 4,096 x 16 73.5 -> 71.3; 2 x 4,096 x 16
-  // (1,024 two-block workgroups) 163.7 -> 165.2.
-  const bool fold = l.moments && sol::folds_moments(cdiv(key_tokens, SOL_BLOCK)) &&
-                    batch * heads * cdiv(cdiv(query_tokens, SOL_BLOCK), 2) <= kFoldMaxPairs;
+  // Moments of 17..255 key blocks: the attention workgroups fold the chunk
+  // sums themselves (the same bits) and the moments_kernel launch goes.
+  // All-in calls, one box, alternating libraries, us: 4,096 tokens x 4 heads
+  // 44.3 -> 43.4, 8,192 x 4 70.9 -> 70.1, 4,096 x 16 73.5 -> 71.3; 2 x 4,096
+  // x 16 163.1 -> 162.1 and 4,096 x 10,000 keys x 24 heads 235.3 -> 233.8
+  // (with the fold's loads issued together, before the query mean).
+  const bool fold = l.moments && sol::folds_moments(cdiv(key_tokens, SOL_BLOCK));
   // Keys of at most one 16-block chunk in rows mode: the centroid tiles alone
   // (pool_blocks_kernel, 16 workgroups per head instead of one per head and
   // K / V), and the attention launch forms the moments from tile 0.
