@@ -44,11 +44,22 @@ namespace {
 //   [rescale]      half 1's P V MFMAs
 // The refill's DMA rounds are spread over the 2 KT score chunks.  Scores
 // start from bias(t) when BIASED (-inf drops a key, log2(len) / c adds a
-// centroid's ln(len) logit term), else from 0.
-template <int D, bool BIASED, typename Bias, typename Refill>
+// centroid's ln(len) logit term), else from 0.  LATE: the bias (0 or -inf
+// only) is added once a half's products are done instead, which keeps it out
+// of the registers live across the score chain; the same values (x + 0 is x
+// for the nonzero-signed sums a chain from +0 gives, and -inf either way).
+template <int D, bool BIASED, typename Bias, typename Refill, bool LATE = false>
 __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
                                             const bf16x8 (&qf)[Shape<D>::KT], int col, int hh, float c,
                                             Bias bias, const Refill& refill) {
+  constexpr bool EARLY = BIASED && !LATE;
+  auto late = [&](f32x16& x, int t) {
+    if constexpr (LATE) {
+      const f32x16 b = bias(t);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) x[e] = x[e] + b[e];
+    }
+  };
   constexpr int KT = Shape<D>::KT, DT = Shape<D>::DT;
   static_assert(KT == 2 * DT, "score and P V chunk counts match");
   const FragLane<D> fl(fresh(col), fresh(hh));
@@ -59,13 +70,14 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
   // The raw scores of half t again (FastHalf::resolve), from the tile still in LDS.
   auto raw = [&](int t) {
     const FragLane<D> fr(fresh(col), fresh(hh));
-    f32x16 s = BIASED ? bias(t) : zero16();
+    f32x16 s = EARLY ? bias(t) : zero16();
 #pragma unroll
     for (int ks = 0; ks < KT; ++ks) s = mfma32x32x16(as_bf16x8(fr.k(buf, t, ks)), qf[ks], s);
+    late(s, t);
     return s;
   };
   FastHalf<D> h0, h1;
-  h0.s = BIASED ? bias(0) : zero16();
+  h0.s = EARLY ? bias(0) : zero16();
   chunk_end();
 #pragma unroll
   for (int ks = 0; ks < KT; ++ks) {
@@ -74,10 +86,11 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
     refill.template after_step<2 * KT>(ks);
     chunk_end();
   }
+  late(h0.s, 0);
   u32x4 va[2][DT];
 #pragma unroll
   for (int ks = 0; ks < KT; ++ks) {
-    if (ks == 0) h1.s = BIASED ? bias(1) : zero16();
+    if (ks == 0) h1.s = EARLY ? bias(1) : zero16();
     h1.s = mfma32x32x16(as_bf16x8(k1[ks]), qf[ks], h1.s);
     h0.template part<KT>(ks, st, c);
     if (ks >= KT / 2) {  // two of half 0's 2 DT = KT V^T fragments per chunk
@@ -89,6 +102,7 @@ __device__ __forceinline__ void tile_attend(State<D>& st, const uint16_t* buf,
     chunk_end();
   }
   h0.resolve(st, c, [&] { return raw(0); });
+  late(h1.s, 1);
   u32x4 vb[2][DT];
 #pragma unroll
   for (int f = 0; f < 2 * DT; ++f) {
@@ -140,17 +154,16 @@ __device__ __forceinline__ void exact_tile(State<D>& st, const uint16_t* buf, in
     full_tile<D>(st, buf, qf, col, hh, c, refill);
   } else {
     const int2 present = tail_rows<SHIFTED>(j, tk, hh);
-    tile_attend<D, true>(st, buf, qf, col, hh, c,
-                         [&](int t) {
-                           f32x16 bias;
+    const auto absent = [&](int t) {
+      f32x16 bias;
 #pragma unroll
-                           for (int e = 0; e < 16; ++e) {
-                             const int row = tile_row(t, e, 0);
-                             bias[e] = row >= present.x && row < present.y ? 0.f : kNegInf;
-                           }
-                           return bias;
-                         },
-                         refill);
+      for (int e = 0; e < 16; ++e) {
+        const int row = tile_row(t, e, 0);
+        bias[e] = row >= present.x && row < present.y ? 0.f : kNegInf;
+      }
+      return bias;
+    };
+    tile_attend<D, true, decltype(absent), Refill, true>(st, buf, qf, col, hh, c, absent, refill);
   }
 }
 
