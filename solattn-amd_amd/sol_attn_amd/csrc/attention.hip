@@ -1358,7 +1358,7 @@ __global__ __launch_bounds__(256, 2) void dense_attention_kernel(AttnParams p) {
   __shared__ __align__(256) uint16_t ring[RING];
 
   const int nq_tiles = (p.Tq + QROWS - 1) / QROWS;
-  const TileTask task = xcd_task(blockIdx.x, nq_tiles);
+  const TileTask task = balanced_task(blockIdx.x, 0, p.B * p.H, nq_tiles);
   if (task.bh < 0) return;
   const int qt = task.tile;
   const int bh = task.bh;
@@ -1468,11 +1468,10 @@ constexpr int64_t kSmallLaunchGroups = 512;
 template <int D, int G, bool SEG>
 void launch_sol_variant(const AttnParams& p, hipStream_t stream) {
   // Grid of sol_task: the sink-holding tiles of every head (p.splits
-  // workgroups each), then xcd_task's.
+  // workgroups each), then balanced_task's.
   const int ntiles = (p.NQB + G - 1) / G, front = std::min(p.q_sink_blocks, ntiles);
   const int split_tiles = sink_split_tiles(p.splits, p.q_sink_blocks, G, front);
-  const unsigned grid = unsigned(split_tiles * (p.splits - 1) + front) * unsigned(p.B * p.H) +
-                        xcd_grid(p.B * p.H, ntiles - front);
+  const unsigned grid = balanced_grid((split_tiles * (p.splits - 1) + front) * (p.B * p.H), p.B * p.H, ntiles - front);
   // Key blocks from pooled tile pairs (p.tiles) or straight from K / V rows.
   if (p.tiles) {
     if (p.k8)
@@ -1551,7 +1550,7 @@ hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
 }
 
 hipError_t launch_dense(const AttnParams& p, int D, hipStream_t stream) {
-  const unsigned grid = xcd_grid(p.B * p.H, (p.Tq + 127) / 128);
+  const unsigned grid = balanced_grid(0, p.B * p.H, (p.Tq + 127) / 128);
   if (D == 128) {
     if (p.tiles)
       hipLaunchKernelGGL((dense_attention_kernel<128, true>), dim3(grid), dim3(256), 0, stream, p);

@@ -18,31 +18,63 @@ constexpr int kXcds = 8;
 
 // Workgroup ids are dealt round-robin over the 8 XCDs.  The id -> (head, query
 // tile) map keeps every XCD on the SAME head at the same time, each on its own
-// contiguous 1/8 slice of the query tiles: neighbouring tiles share that XCD's
-// L2, and the tiles of one head (43 MB at 84,672 tokens) are the whole live
-// set of the memory-side cache.  Grid = 8 * heads * slice; ids past the end of
-// a slice return -1 (idle workgroup).
+// contiguous slice of that head's query tiles: neighbouring tiles share that
+// XCD's L2, and the tiles of one head (43 MB at 84,672 tokens) are the whole
+// live set of the memory-side cache.  The first F ids (a SOL launch's
+// query-sink tiles, sol_task) go ahead of that map; after them, XCD x's
+// workgroups take, head after head, its slice of the head's R tiles: floor(R
+// / 8) tiles, one more for the XCDs that the R mod 8 leftover tiles of each
+// head are dealt to -- round-robin, continuing from the F front ids -- so that
+// every XCD holds the same number of workgroups to within one.  (Equal
+// ceil(R / 8) slices with the last XCD short left 7 XCDs a workgroup round
+// more than the eighth when R mod 8 != 0, or when the front ids fell on
+// them: at 32,768 tokens x 4 heads with 128-token sinks, 129 workgroups
+// against 64 slots per XCD.)  Ids past an XCD's count return -1 (idle).
 struct TileTask {
   int bh, tile;
   int split = 0;  // key-range part of a split front tile (sol_task)
 };
 
-__device__ __forceinline__ TileTask xcd_task(int i, int ntiles) {
-  const int slice = (ntiles + kXcds - 1) / kXcds;
-  const int xcd = i % kXcds, k = i / kXcds;
-  const int tile = xcd * slice + k % slice;
-  return TileTask{tile < ntiles ? k / slice : -1, tile};
+// Regular workgroup id i >= F: (head, tile in [0, R)) as described above.
+__device__ __forceinline__ TileTask balanced_task(int i, int F, int heads, int R) {
+  const int x = i % kXcds, k = i / kXcds;
+  const int fx = F > x ? (F - x + kXcds - 1) / kXcds : 0;  // front ids of XCD x
+  const int kr = k - fx;                                    // its regular index
+  const int base = R / kXcds, rem = R % kXcds;
+  const int r0 = ((x - F) % kXcds + kXcds) % kXcds;  // leftover e goes to XCD (F + e) % 8
+  // XCD x's regular workgroups in heads [0, h).
+  auto cum = [&](int h) {
+    const int n = h * rem;
+    return h * base + (n > r0 ? (n - 1 - r0) / kXcds + 1 : 0);
+  };
+  int h = R > 0 ? min(heads, int(int64_t(kr) * kXcds / R)) : heads;
+  while (h > 0 && cum(h) > kr) --h;
+  while (h < heads && cum(h + 1) <= kr) ++h;
+  if (h >= heads || kr < 0) return TileTask{-1, 0};
+  // Start of XCD x's slice of head h: the slices of XCDs 0 .. x-1, of which
+  // those in [c, c + rem) (mod 8) hold one leftover tile more.
+  const int c = (F + h * rem) % kXcds;
+  const int extra_before = c + rem <= kXcds ? max(0, min(x, c + rem) - c)
+                                            : max(0, x - c) + min(x, c + rem - kXcds);
+  return TileTask{h, x * base + extra_before + (kr - cum(h))};
+}
+
+// Workgroups of a launch of F front ids and `heads` x R regular tiles: every
+// XCD's count, rounded up, eight times.
+__host__ __device__ inline unsigned balanced_grid(int F, int heads, int R) {
+  const int64_t total = int64_t(F) + int64_t(heads) * R;
+  return unsigned(kXcds * ((total + kXcds - 1) / kXcds));
 }
 
 // SOL launches dispatch the first `front` query tiles of every (entry, head)
 // ahead of the rest, head-interleaved.  With query sinks those tiles hold the
 // sink query blocks, whose workgroups stream every key block and run several
-// times longer than the others; in xcd_task order the last heads' ones would
-// start late and set the kernel's end (2 x 4,096 tokens x 16 heads with
+// times longer than the others; behind the regular map the last heads' ones
+// would start late and set the kernel's end (2 x 4,096 tokens x 16 heads with
 // 128-token sinks: 251 -> 163 us).  The first `split_tiles` of them (<=
 // front) are `splits` workgroups each, one per key range (split_range), whose
-// partial states sol_merge_kernel combines.  The remaining tiles keep the
-// xcd_task map.
+// partial states sol_merge_kernel combines.  The remaining tiles follow
+// balanced_task.
 __device__ __forceinline__ TileTask sol_task(int i, int ntiles, int front, int split_tiles, int heads,
                                              int splits) {
   const int nsplit = split_tiles * heads * splits;
@@ -50,11 +82,9 @@ __device__ __forceinline__ TileTask sol_task(int i, int ntiles, int front, int s
     const int j = i / heads;
     return TileTask{i % heads, j / splits, j % splits};
   }
-  i -= nsplit;
   const int nrest = (front - split_tiles) * heads;
-  if (i < nrest) return TileTask{i % heads, split_tiles + i / heads};
-  if (ntiles <= front) return TileTask{-1, 0};
-  TileTask t = xcd_task(i - nrest, ntiles - front);
+  if (i - nsplit < nrest) return TileTask{(i - nsplit) % heads, split_tiles + (i - nsplit) / heads};
+  TileTask t = balanced_task(i, nsplit + nrest, heads, ntiles - front);
   t.tile += front;
   return t;
 }
@@ -74,9 +104,7 @@ __device__ __forceinline__ int2 split_range(int s, int n, int nkb) {
   return int2{int(int64_t(s) * nkb / n), int(int64_t(s + 1) * nkb / n)};
 }
 
-__host__ __device__ inline unsigned xcd_grid(int heads, int ntiles) {
-  return unsigned(kXcds) * unsigned(heads) * unsigned((ntiles + kXcds - 1) / kXcds);
-}
+
 
 template <int D>
 struct Shape {
