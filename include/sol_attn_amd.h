@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SOL_ABI_VERSION 13
+#define SOL_ABI_VERSION 14
 #define SOL_BLOCK 64                /* tokens per physical block, kernels.py:12 */
 #define SOL_MAX_KEY_TOKENS (1ll << 25) /* key_tokens of one pooling call (2^19 key blocks) */
 
@@ -156,7 +156,11 @@ int64_t sol_split_workspace_size(int64_t batch, int64_t query_tokens, int64_t ke
  * -INFINITY, which selects every block, or an invalid shape): the routing
  * decisions, uint32 [batch, heads, ceil(query_tokens / 64), ceil(NKB / 32)]
  * (bit j of word w: key block 32 w + j), written by the routing kernel and
- * read by the attention kernel of the same call. */
+ * read by the attention kernel of the same call; then, 256-byte aligned,
+ * int32 [batch, heads, ceil(query_tokens / 64)]: the order in which a
+ * two-block launch hands its query tiles to the XCDs, formed from the
+ * decisions (costly tiles first, each XCD's share of every head balanced;
+ * the results do not depend on it). */
 int64_t sol_route_workspace_size(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
                                  double beta);
 

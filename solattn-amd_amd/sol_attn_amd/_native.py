@@ -18,7 +18,7 @@ import threading
 import torch
 
 BLOCK = 64
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libsol_attn_amd.so")

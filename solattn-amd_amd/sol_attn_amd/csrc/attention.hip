@@ -656,8 +656,10 @@ __global__ __launch_bounds__(256, 2) void sol_attention_kernel(AttnParams p) {
   const int ntiles = (p.NQB + G - 1) / G;
   const int front = min(p.q_sink_blocks, ntiles);
   const int split_tiles = sink_split_tiles(p.splits, p.q_sink_blocks, G, front);
-  const TileTask task = sol_task(blockIdx.x, ntiles, front, split_tiles, p.B * p.H, p.splits);
+  TileTask task = sol_task(blockIdx.x, ntiles, front, split_tiles, p.B * p.H, p.splits);
   if (task.bh < 0) return;
+  if (G == 2 && p.order && task.tile >= front)  // the order_kernel's deal of the regular tiles
+    task.tile = front + p.order[int64_t(task.bh) * p.NQB + task.tile - front];
   const int bh = task.bh;
   const int h = bh % p.H, b = bh / p.H;
   const int64_t head = int64_t(b) * p.H + h;
@@ -1455,6 +1457,61 @@ __global__ __launch_bounds__(kMergeThreads) void sol_merge_kernel(AttnParams p, 
   *reinterpret_cast<u32x2*>(p.out + (orow * p.H + h) * D + 4 * c) = v;
 }
 
+// Order of the R regular query tiles of a two-block launch whose routing
+// masks are known before it (route_kernel): a tile's cost is its union of
+// selected key blocks, and per (entry, head) the tiles are ranked by falling
+// cost (ties by index) and dealt to the XCD slices of balanced_task in snake
+// order (rank 0 .. 7 to XCDs 0 .. 7, ranks 8 .. 15 to XCDs 7 .. 0, ...; the R
+// mod 8 cheapest to the XCDs with a leftover slot), each slice taking its
+// tiles in falling cost.  Every XCD then holds about the same work of each
+// head, the costly workgroups start first, and the grid's tail is short.
+// order[bh NQB + slot] = the regular tile of that slot.  A permutation:
+// results do not depend on it.  One workgroup per (entry, head).
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderMaxTiles = 4096;
+
+__global__ __launch_bounds__(kOrderThreads) void order_kernel(AttnParams p, int front, int F) {
+  __shared__ uint32_t s_cost[kOrderMaxTiles];
+  const int bh = blockIdx.x;
+  const int ntiles = (p.NQB + 1) / 2, R = ntiles - front;
+  const int stride = p.pair_stride ? min(p.pair_stride[bh], p.NQB) : 0;
+  const uint32_t* mask = p.mask + int64_t(bh) * p.NQB * p.NW;
+  for (int r = threadIdx.x; r < R; r += kOrderThreads) {
+    const int t = front + r;
+    const int a = slot_block(2 * t, p.NQB, stride), b = slot_block(2 * t + 1, p.NQB, stride);
+    uint32_t n = 0;
+    for (int w = 0; w < p.NW; ++w) {
+      uint32_t m = mask[int64_t(a) * p.NW + w];
+      if (b < p.NQB) m |= mask[int64_t(b) * p.NW + w];
+      n += __builtin_popcount(m);
+    }
+    s_cost[r] = n;
+  }
+  __syncthreads();
+  const int base = R / kXcds, rem = R % kXcds;
+  const int c = int((int64_t(F) + int64_t(bh) * rem) % kXcds);  // first XCD with a leftover slot
+  for (int r = threadIdx.x; r < R; r += kOrderThreads) {
+    const uint32_t cr = s_cost[r];
+    int rank = 0;
+    for (int q = 0; q < R; ++q) {
+      const uint32_t cq = s_cost[q];
+      rank += (cq > cr || (cq == cr && q < r)) ? 1 : 0;
+    }
+    int x, j;
+    if (rank < kXcds * base) {
+      const int round = rank / kXcds, q = rank % kXcds;
+      x = (round & 1) ? kXcds - 1 - q : q;
+      j = round;
+    } else {
+      x = (c + rank - kXcds * base) % kXcds;
+      j = base;
+    }
+    const int extra_before = c + rem <= kXcds ? max(0, min(x, c + rem) - c)
+                                              : max(0, x - c) + min(x, c + rem - kXcds);
+    p.order[int64_t(bh) * p.NQB + x * base + extra_before + j] = r;
+  }
+}
+
 // LDS ring depth of the SOL kernel.
 constexpr int kSolRing = 2;
 // Below this many two-block workgroups the launch leaves CUs idle (256 CUs x
@@ -1541,10 +1598,22 @@ hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
   }
   int g = int64_t(p.B) * p.H * ((p.NQB + 1) / 2) < kSmallLaunchGroups ? 1 : 2;
   if (p.workgroup_form == 1 || p.workgroup_form == 2) g = p.workgroup_form;
+  AttnParams q = p;
+  q.order = nullptr;
+  if (g == 2 && p.order && p.mask && p.force != 1 && p.splits == 1) {
+    const int ntiles = (p.NQB + 1) / 2, front = std::min(p.q_sink_blocks, ntiles);
+    if (ntiles - front > 0 && ntiles - front <= kOrderMaxTiles) {
+      hipLaunchKernelGGL(order_kernel, dim3(unsigned(p.B * p.H)), dim3(kOrderThreads), 0, stream, p, front,
+                         front * p.B * p.H);
+      const hipError_t err = hipGetLastError();
+      if (err != hipSuccess) return err;
+      q.order = p.order;
+    }
+  }
   if (D == 128) {
-    if (g == 1) launch_sol_group<128, 1>(p, stream); else launch_sol_group<128, 2>(p, stream);
+    if (g == 1) launch_sol_group<128, 1>(q, stream); else launch_sol_group<128, 2>(q, stream);
   } else {
-    if (g == 1) launch_sol_group<64, 1>(p, stream); else launch_sol_group<64, 2>(p, stream);
+    if (g == 1) launch_sol_group<64, 1>(q, stream); else launch_sol_group<64, 2>(q, stream);
   }
   return hipGetLastError();
 }

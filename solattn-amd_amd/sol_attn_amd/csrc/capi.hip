@@ -87,6 +87,12 @@ int scratch_on_current_device(void** ptr) {
 int64_t align256(int64_t n) { return (n + 255) / 256 * 256; }
 
 // Routing masks of sol_attention_fwd: uint32 [batch, heads, NQB, ceil(NKB / 32)].
+// Tile order of sol_attention_fwd's route workspace (after the masks): int32
+// [batch, heads, NQB].
+int64_t route_order_bytes(int64_t batch, int64_t query_tokens, int64_t heads) {
+  return batch * heads * cdiv(query_tokens, SOL_BLOCK) * 4;
+}
+
 int64_t route_mask_bytes(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads) {
   return batch * heads * cdiv(query_tokens, SOL_BLOCK) * cdiv(cdiv(key_tokens, SOL_BLOCK), 32) * 4;
 }
@@ -404,7 +410,7 @@ int64_t sol_route_workspace_size(int64_t batch, int64_t query_tokens, int64_t ke
       std::isnan(beta))
     return 0;
   if (std::isinf(beta) && beta < 0) return 0;  // every block exact: no routing
-  return route_mask_bytes(batch, query_tokens, key_tokens, heads);
+  return align256(route_mask_bytes(batch, query_tokens, key_tokens, heads)) + route_order_bytes(batch, query_tokens, heads);
 }
 
 int sol_attention_pools_keys(int64_t batch, int64_t query_tokens, int64_t key_tokens, int64_t heads,
@@ -627,6 +633,9 @@ int attention_fwd_impl(const void* q, const int64_t* q_strides, const int64_t* q
   p.splits = split_workspace ? sink_splits(batch * heads, nqb, nkb, p.q_sink_blocks, force, head_dim) : 1;
   p.partial = p.splits > 1 ? static_cast<float*>(split_workspace) : nullptr;
   p.mask = force != 1 ? static_cast<uint32_t*>(route_workspace) : nullptr;
+  p.order = p.mask ? reinterpret_cast<int32_t*>(static_cast<uint8_t*>(route_workspace) +
+                                                align256(route_mask_bytes(batch, query_tokens, key_tokens, heads)))
+                   : nullptr;
   p.NW = int(cdiv(nkb, 32));
   p.qc = query_means;
   return hip_status(sol::launch_sol(p, int(head_dim), static_cast<hipStream_t>(stream)));

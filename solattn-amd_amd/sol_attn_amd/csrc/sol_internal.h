@@ -103,6 +103,8 @@ struct AttnParams {
                        // null: the attention kernel routes tile by tile
   int NW;              // ceil(NKB / 32)
   const float* qc;     // [B, H, NQB, D] FP32 query-block means for route_kernel, or null (formed from Q)
+  int32_t* order;      // [B H, NQB] with mask: the regular query tiles of a two-block launch in
+                       // the order order_kernel deals them to the XCDs, or null: tile order
 };
 
 // Indexed-window protection (plan.hip).

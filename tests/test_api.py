@@ -145,7 +145,7 @@ def test_c_abi_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     assert set(names) == set(_native._SIGNATURES)
     native = _native.library()
-    assert native.sol_abi_version() == _native.ABI_VERSION == 13
+    assert native.sol_abi_version() == _native.ABI_VERSION == 14
     sizes = (ctypes.c_int64 * 4)()
     assert native.sol_pool_sizes(1, 317, 2, 64, sizes) == 0
     tile = 2 * 64 * 64 * 2
