@@ -1466,37 +1466,57 @@ __global__ __launch_bounds__(kMergeThreads) void sol_merge_kernel(AttnParams p, 
 // tiles in falling cost.  Every XCD then holds about the same work of each
 // head, the costly workgroups start first, and the grid's tail is short.
 // order[bh NQB + slot] = the regular tile of that slot.  A permutation:
-// results do not depend on it.  One workgroup per (entry, head).
+// results do not depend on it.
+// kOrderParts workgroups per (entry, head): each forms every tile's cost
+// (the mask words read eight at a time, so the loads overlap) and ranks one
+// part of the tiles, kRankLanes adjacent lanes per tile, each counting over
+// a strided share of the other tiles, their counts summed with shuffles.
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderMaxTiles = 4096;
+constexpr int kOrderParts = 8;
+constexpr int kRankLanes = 8;
+static_assert(kOrderThreads % kRankLanes == 0 && kWave % kRankLanes == 0, "rank groups stay inside a wave");
 
 __global__ __launch_bounds__(kOrderThreads) void order_kernel(AttnParams p, int front, int F) {
   __shared__ uint32_t s_cost[kOrderMaxTiles];
-  const int bh = blockIdx.x;
+  const int bh = blockIdx.x / kOrderParts, part = blockIdx.x % kOrderParts;
   const int ntiles = (p.NQB + 1) / 2, R = ntiles - front;
   const int stride = p.pair_stride ? min(p.pair_stride[bh], p.NQB) : 0;
   const uint32_t* mask = p.mask + int64_t(bh) * p.NQB * p.NW;
   for (int r = threadIdx.x; r < R; r += kOrderThreads) {
     const int t = front + r;
     const int a = slot_block(2 * t, p.NQB, stride), b = slot_block(2 * t + 1, p.NQB, stride);
+    const uint32_t* ma = mask + int64_t(a) * p.NW;
+    const uint32_t* mb = b < p.NQB ? mask + int64_t(b) * p.NW : ma;  // no partner: its own words
     uint32_t n = 0;
-    for (int w = 0; w < p.NW; ++w) {
-      uint32_t m = mask[int64_t(a) * p.NW + w];
-      if (b < p.NQB) m |= mask[int64_t(b) * p.NW + w];
-      n += __builtin_popcount(m);
+    int w = 0;
+    for (; w + 8 <= p.NW; w += 8) {
+      uint32_t m[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) m[u] = ma[w + u] | mb[w + u];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) n += __builtin_popcount(m[u]);
     }
+    for (; w < p.NW; ++w) n += __builtin_popcount(ma[w] | mb[w]);
     s_cost[r] = n;
   }
   __syncthreads();
   const int base = R / kXcds, rem = R % kXcds;
   const int c = int((int64_t(F) + int64_t(bh) * rem) % kXcds);  // first XCD with a leftover slot
-  for (int r = threadIdx.x; r < R; r += kOrderThreads) {
+  const int chunk = (R + kOrderParts - 1) / kOrderParts;
+  const int r0 = part * chunk, r1 = min(R, r0 + chunk);
+  const int tasks = max(0, r1 - r0) * kRankLanes;  // whole rank groups: a group is all in or all out
+  for (int task = threadIdx.x; task < tasks; task += kOrderThreads) {
+    const int r = r0 + task / kRankLanes, sub = task % kRankLanes;
     const uint32_t cr = s_cost[r];
     int rank = 0;
-    for (int q = 0; q < R; ++q) {
+    for (int q = sub; q < R; q += kRankLanes) {
       const uint32_t cq = s_cost[q];
       rank += (cq > cr || (cq == cr && q < r)) ? 1 : 0;
     }
+#pragma unroll
+    for (int off = 1; off < kRankLanes; off <<= 1) rank += __shfl_xor(rank, off);
+    if (sub != 0) continue;
     int x, j;
     if (rank < kXcds * base) {
       const int round = rank / kXcds, q = rank % kXcds;
@@ -1603,8 +1623,8 @@ hipError_t launch_sol(const AttnParams& p, int D, hipStream_t stream) {
   if (g == 2 && p.order && p.mask && p.force != 1 && p.splits == 1) {
     const int ntiles = (p.NQB + 1) / 2, front = std::min(p.q_sink_blocks, ntiles);
     if (ntiles - front > 0 && ntiles - front <= kOrderMaxTiles) {
-      hipLaunchKernelGGL(order_kernel, dim3(unsigned(p.B * p.H)), dim3(kOrderThreads), 0, stream, p, front,
-                         front * p.B * p.H);
+      hipLaunchKernelGGL(order_kernel, dim3(unsigned(p.B * p.H * kOrderParts)), dim3(kOrderThreads), 0, stream, p,
+                         front, front * p.B * p.H);
       const hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
       q.order = p.order;
