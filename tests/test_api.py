@@ -184,7 +184,12 @@ def test_c_abi_rejects_bad_arguments_without_launching():
                                   fake, None, None, None, None, None, None, None, 0, None)
     assert rc == -1 and b"query_means" in native.sol_last_error()
     assert native.sol_route_workspace_size(1, 193, 317, 2, float("-inf")) == 0
-    assert native.sol_route_workspace_size(2, 193, 317, 3, 1.0) == 2 * 3 * 4 * 1 * 4
+    # Decision words [B, H, NQB, ceil(NKB / 32)], then, 256-byte aligned, the
+    # int32 tile order [B, H, NQB].
+    mask_bytes = 2 * 3 * 4 * 1 * 4
+    assert native.sol_route_workspace_size(2, 193, 317, 3, 1.0) == -(-mask_bytes // 256) * 256 + 2 * 3 * 4 * 4
+    assert native.sol_route_workspace_size(1, 64 * 100, 64 * 70, 2, 0.5) == \
+        -(-(1 * 2 * 100 * 3 * 4) // 256) * 256 + 1 * 2 * 100 * 4
     assert attn(None, 0, 3) == -1 and b"workgroup_form" in native.sol_last_error()
     assert attn(fake, 0, 0) == -1 and b"sequence_length" in native.sol_last_error()
     # Without tiles the keys must qualify for rows mode.
