@@ -105,39 +105,56 @@ __global__ __launch_bounds__(kMeanThreads) void qblock_means_kernel(PairParams p
 }
 
 // Lag sums of one feature d of one (batch entry, head): thread t holds the
-// four lags s = 4 t + 1 .. 4 t + 4, sum over i of m_i[d] m_{i+s}[d].  The
-// thread slides a four-value register window over m_{i+s}, so each step
-// reads m_i (the same for every lane) and one new window value.  The LDS copy
-// is zero-padded past NQB, so terms past the end add exact zeros.
+// four lags s = 4 t + 1 .. 4 t + 4, sum over i of m_i[d] m_{i+s}[d], each
+// in ascending i.  Steps go four at a time: a step block needs m_i .. m_{i+3}
+// (the same for every lane) and the lane's window m_{i+s0} .. m_{i+s0+7}, of
+// which the first four came with the previous block, and the reads for the
+// next block are issued before this block's products, so their latency
+// overlaps them.  The LDS copy is zero-padded past NQB (kLagPad values, enough
+// for the block after the last), so terms past the end add exact zeros.
+// Value k sits at word lag_word(k) = k + k / 32: the lanes' window reads lie
+// 4 values apart, and without the pad word after every 32 values groups of 8
+// lanes would hit the same bank; with it the lanes 8 apart fall in
+// neighbouring banks.
 constexpr int kLagThreads = kMaxLag / 4;
-constexpr int kLagPad = kMaxLag + 4;
+constexpr int kLagPad = kMaxLag + 16;
+
+__host__ __device__ constexpr int lag_word(int k) { return k + (k >> 5); }
 
 __global__ __launch_bounds__(kLagThreads) void pair_lag_kernel(PairParams p, int D) {
-  extern __shared__ float x[];  // NQB + kLagPad floats
+  extern __shared__ float x[];  // lag_word(NQB + kLagPad - 1) + 1 floats
   const int d = blockIdx.x, bh = blockIdx.y, n = p.NQB;
   const float* src = p.means + (int64_t(bh) * D + d) * n;
-  for (int i = threadIdx.x; i < n + kLagPad; i += kLagThreads) x[i] = i < n ? src[i] : 0.f;
+  for (int i = threadIdx.x; i < n + kLagPad; i += kLagThreads) x[lag_word(i)] = i < n ? src[i] : 0.f;
   __syncthreads();
   const int s0 = 4 * threadIdx.x + 1;
-  float w0 = x[s0], w1 = x[s0 + 1], w2 = x[s0 + 2], w3 = x[s0 + 3];  // m_{i+s0 .. i+s0+3}, i = 0
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll 4
-  for (int i = 0; i < n; ++i) {
-    const float xi = x[i];
-    a0 = fmaf(xi, w0, a0);
-    a1 = fmaf(xi, w1, a1);
-    a2 = fmaf(xi, w2, a2);
-    a3 = fmaf(xi, w3, a3);
-    w0 = w1;
-    w1 = w2;
-    w2 = w3;
-    w3 = x[i + s0 + 4];
+  float v[8], xc[4];  // v: m_{i+s0} .. m_{i+s0+7}; xc: m_i .. m_{i+3}
+#pragma unroll
+  for (int u = 0; u < 8; ++u) v[u] = x[lag_word(s0 + u)];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) xc[u] = x[lag_word(u)];
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < n; i += 4) {
+    float xn[4], wn[4];  // the next block's m_{i+4} .. m_{i+7} and m_{i+s0+8} .. m_{i+s0+11}
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      xn[u] = x[lag_word(i + 4 + u)];
+      wn[u] = x[lag_word(i + s0 + 8 + u)];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a[k] = fmaf(xc[u], v[u + k], a[k]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      xc[u] = xn[u];
+      v[u] = v[u + 4];
+      v[u + 4] = wn[u];
+    }
   }
   float* dst = p.lags + (int64_t(bh) * D + d) * kMaxLag + 4 * threadIdx.x;
-  dst[0] = a0;
-  dst[1] = a1;
-  dst[2] = a2;
-  dst[3] = a3;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) dst[k] = a[k];
 }
 
 // Per (batch entry, head): mean cosine per lag, pairing score per stride,
@@ -174,8 +191,8 @@ hipError_t launch_pairing(const PairParams& p, int D, hipStream_t stream) {
     hipLaunchKernelGGL(qblock_means_kernel<128>, dim3(mean_grid), dim3(kMeanThreads), 0, stream, p);
   else
     hipLaunchKernelGGL(qblock_means_kernel<64>, dim3(mean_grid), dim3(kMeanThreads), 0, stream, p);
-  hipLaunchKernelGGL(pair_lag_kernel, dim3(D, p.B * p.H), dim3(kLagThreads), (p.NQB + kLagPad) * sizeof(float),
-                     stream, p, D);
+  hipLaunchKernelGGL(pair_lag_kernel, dim3(D, p.B * p.H), dim3(kLagThreads),
+                     (lag_word(p.NQB + kLagPad - 1) + 1) * sizeof(float), stream, p, D);
   hipLaunchKernelGGL(pair_pick_kernel, dim3(p.B * p.H), dim3(kMaxLag), 0, stream, p, D);
   return hipGetLastError();
 }
