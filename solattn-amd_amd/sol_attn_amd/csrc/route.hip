@@ -38,7 +38,7 @@ namespace {
 
 constexpr int kRouteThreads = 256;  // four waves
 constexpr int kRouteBlocks = 32;    // query blocks per workgroup: the MFMA tile's columns
-constexpr int kRouteChunks = 16;    // 32-key-block chunks per workgroup when Qc comes from p.qc
+constexpr int kRouteChunks = 24;    // 32-key-block chunks per workgroup when Qc comes from p.qc
 constexpr float kInf = __builtin_huge_valf();
 
 // FP32 -> BF16 bits, round to nearest even, and back.
