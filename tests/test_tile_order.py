@@ -11,8 +11,9 @@ inside every XCD's slice the costs do not rise; the j-th tile of a slice lies
 between the costs of ranks 8j and 8j + 7 (each round of eight ranks goes to
 eight different XCDs); the leftover slots hold the cheapest tiles.  Outputs
 and counts are bit-identical to the one-block workgroup form (no order) under
-the same routing masks, with and without query-block pairing, and match the
-oracle under the kernel's routing.
+the same routing masks, with and without query-block pairing and for keys
+past one routing segment (8,192 key blocks), and match the oracle under the
+kernel's routing.
 """
 
 import numpy as np
@@ -116,3 +117,21 @@ def test_ordered_paired_launch_matches_one_block_form_and_oracle(monkeypatch):
     actual, ref, _ = check_routing(q, k, v, 1.0, kv_sink=64, q_sink=128, local=1, label="ordered tiles")
     assert_close(actual, ref)
     assert (actual == to_np(two)).all()     # the debug launch (same masks, same order) gives the same output
+
+
+def test_ordered_tiles_across_routing_segments(monkeypatch):
+    """Keys past one routing segment (8,192 key blocks): the order kernel
+    counts every segment's mask words; outputs equal the one-block form's."""
+    tq, tk, h, d = 2200, 8192 * 64 + 300 * 64 + 17, 1, 128   # 35 query blocks: 17 regular tiles
+    gen = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(1, t, h, d, generator=gen).to(torch.bfloat16).cuda() for t in (tq, tk, tk))
+    print(f"tile order across segments: Tq {tq} Tk {tk}", flush=True)
+    monkeypatch.setattr(_native, "PAIRING", False)
+    keep = []
+    two, counts2 = _run(q, k, v, 2, monkeypatch, beta=0.0, q_sink=64, keep=keep)
+    assert len(keep) == 1
+    cost = _check_order(keep[0], 1, tq, tk, h, 64)
+    assert cost.max() > cost.min()
+    one, counts1 = _run(q, k, v, 1, monkeypatch, beta=0.0, q_sink=64)
+    assert torch.equal(one, two)
+    assert torch.equal(counts1, counts2)
