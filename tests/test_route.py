@@ -29,7 +29,9 @@ def prepass(monkeypatch):
 @pytest.mark.parametrize("beta", [0.0, 1.0, math.inf])
 @pytest.mark.parametrize("case", [dict(nq=300, nk=517, d=128, b=1, h=2, strided=True),
                                   dict(nq=777, nk=1500, d=64, b=2, h=3),
-                                  dict(nq=1024, nk=4000, d=128, b=1, h=2)])
+                                  dict(nq=1024, nk=4000, d=128, b=1, h=2),
+                                  # 782 key blocks = 25 chunks of 32: two key ranges per query-block group
+                                  dict(nq=640, nk=50000, d=64, b=1, h=2)])
 def test_routing_kernel_against_oracle(prepass, case, beta, means):
     if means == "pairing":
         prepass.setattr(_native, "PAIR_MIN_QUERY_BLOCKS", 1)   # pairing also writes the query means
