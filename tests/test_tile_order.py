@@ -135,3 +135,21 @@ def test_ordered_tiles_across_routing_segments(monkeypatch):
     one, counts1 = _run(q, k, v, 1, monkeypatch, beta=0.0, q_sink=64)
     assert torch.equal(one, two)
     assert torch.equal(counts1, counts2)
+
+
+def test_order_at_the_largest_ordered_launch(monkeypatch):
+    """4,096 regular tiles per head (8,192 query blocks), the most the order
+    kernel takes: still a balanced permutation, outputs equal to the
+    one-block form's."""
+    t, h, d = 8192 * 64, 1, 64
+    q, k, v = (block_smooth(1, t, h, d, seed=s, device="cuda") for s in (41, 42, 43))
+    print(f"tile order: {t} tokens, 4,096 tiles per head", flush=True)
+    monkeypatch.setattr(_native, "PAIRING", False)
+    keep = []
+    two, counts2 = _run(q, k, v, 2, monkeypatch, q_sink=0, keep=keep)
+    assert len(keep) == 1
+    cost = _check_order(keep[0], 1, t, t, h, 0)
+    assert cost.max() > cost.min()
+    one, counts1 = _run(q, k, v, 1, monkeypatch, q_sink=0)
+    assert torch.equal(one, two)
+    assert torch.equal(counts1, counts2)
